@@ -1,0 +1,365 @@
+"""Benchmark of the per-block hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S]
+
+Prints ONE JSON line.  The headline workload (`value`) is configs[1] of
+the fused QK-RMSNorm + 3-axis RoPE at the 1024^2 shape
+(Q, K bf16 [1, 4352, 24, 128]), reported as algorithmic HBM GB/s.  The other
+configurations (AdaLN @512^2, SwiGLU, gated residual, MXFP8 quantize, MXFP8
+GEMM + bias, the block minus attention @2048^2 and µs/block @1024^2) are
+measured in the same run and reported under "components".
+
+Timing: each step is one pass of the op over one batch of synthetic input
+already resident in device memory.  The K timed steps are captured in a HIP
+graph (so host launch overhead is not measured) and bracketed by events on the
+launch stream, with torch.cuda.synchronize() on both sides.  Bandwidth-bound
+steps rotate through enough copies of their inputs that the working set
+exceeds the 256 MB Infinity Cache, so the figures are HBM figures.
+
+The CPU baseline is this repository's C oracle (a port of the reference's
+eager semantics) run on the host cores of the same box on a bounded sample.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "qwen-image-2.1-accel_amd"))
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+MXFP8_PEAK_TFLOPS = 5000.0     # MI355X dense MXFP8 MFMA (5.0 PFLOP/s)
+MALL_BYTES = 256 << 20         # Infinity Cache
+METRIC = json.load(open(os.path.join(ROOT, "BASELINE.json")))["metric"]
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class Timed:
+    """Capture `steps` calls of fn(i) (i = step index, for input rotation) in a
+    HIP graph, warm up, then time one replay with events."""
+
+    def __init__(self, fn, steps, warmup):
+        self.fn, self.steps, self.warmup = fn, steps, warmup
+
+    def run(self):
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for i in range(2):                       # eager warm-up (first-call setup)
+                self.fn(i)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(self.steps):
+                self.fn(i)
+        for _ in range(max(1, self.warmup // max(1, self.steps))):
+            graph.replay()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record()
+        graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(end)
+        del graph
+        return ms / self.steps
+
+
+def copies_for(nbytes):
+    """Number of input copies whose total exceeds twice the Infinity Cache."""
+    return max(1, int(np.ceil(2 * MALL_BYTES / max(nbytes, 1))))
+
+
+def gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def randn(g, shape, scale=1.0, dev="cuda"):
+    return (torch.randn(shape, generator=g) * scale).to(torch.bfloat16).to(dev)
+
+
+# ----------------------------------------------------------------- configs --
+
+def bench_adaln(steps, warmup):
+    """Config 1: AdaLN (LN, (1+scale), shift, gate, residual) @512^2."""
+    from qwen_image_accel import _native
+    g = gen(717)
+    M, D = 1280, 3072
+    nbytes = 3 * M * D * 2 + 3 * D * 2
+    n = copies_for(2 * M * D * 2)
+    xs = [randn(g, (M, D)) for _ in range(n)]
+    rs = [randn(g, (M, D)) for _ in range(n)]
+    shift, scale, gate = (randn(g, (1, D), 0.1) for _ in range(3))
+    outs = [torch.empty(M, D, dtype=torch.bfloat16, device="cuda") for _ in range(n)]
+    L = _native.lib()
+
+    def step(i):
+        j = i % n
+        rc = L.qim_adaln(xs[j].data_ptr(), scale.data_ptr(), shift.data_ptr(), gate.data_ptr(),
+                         rs[j].data_ptr(), outs[j].data_ptr(), M, D, M, 1e-6, _native.ADALN_ADD_ONE,
+                         torch.cuda.current_stream().cuda_stream)
+        assert rc == 0
+    us = Timed(step, steps, warmup).run() * 1e3
+    return dict(kernel="qim_adaln", us=us, bytes=nbytes, gbs=nbytes / us / 1e3,
+                frac=nbytes / us / 1e3 / HBM_PEAK_GBS, shape="x,res [1,1280,3072]")
+
+
+def bench_qk_norm_rope(steps, warmup):
+    """Config 2: QK-RMSNorm + 3-axis RoPE @1024^2 (the headline workload)."""
+    from qwen_image_accel import _native, rope
+    g = gen(721)
+    S, H, Dh = 4352, 24, 128
+    nbytes = 4 * S * H * Dh * 2 + S * 64 * 8 + 2 * Dh * 2
+    n = copies_for(2 * S * H * Dh * 2)
+    qs = [randn(g, (1, S, H, Dh)) for _ in range(n)]
+    ks = [randn(g, (1, S, H, Dh)) for _ in range(n)]
+    wq = ((torch.rand(Dh, generator=g) * 0.4 + 0.8).to(torch.bfloat16)).cuda()
+    wk = ((torch.rand(Dh, generator=g) * 0.4 + 0.8).to(torch.bfloat16)).cuda()
+    freqs = torch.view_as_real(rope.image_table(256, 64, 64)).contiguous().cuda()
+    oqs = [torch.empty_like(qs[0]) for _ in range(n)]
+    oks = [torch.empty_like(qs[0]) for _ in range(n)]
+    L = _native.lib()
+
+    def step(i):
+        j = i % n
+        rc = L.qim_qk_norm_rope_pack(qs[j].data_ptr(), ks[j].data_ptr(), None, None, None, wq.data_ptr(),
+                                     wk.data_ptr(), freqs.data_ptr(), oqs[j].data_ptr(), oks[j].data_ptr(),
+                                     None, 1, S, 0, H, Dh, H * Dh, 1e-6, 1e-6,
+                                     torch.cuda.current_stream().cuda_stream)
+        assert rc == 0
+    us = Timed(step, steps, warmup).run() * 1e3
+    return dict(kernel="qim_qk_norm_rope_pack", us=us, bytes=nbytes, gbs=nbytes / us / 1e3,
+                frac=nbytes / us / 1e3 / HBM_PEAK_GBS, shape="Q,K [1,4352,24,128]")
+
+
+def bench_swiglu(steps, warmup):
+    """Config 3a: SwiGLU over the two halves of [4352, 2x12288]."""
+    from qwen_image_accel import _native
+    g = gen(91)
+    M, F = 4352, 12288
+    nbytes = 2 * M * 2 * F + 2 * M * F
+    n = copies_for(2 * M * 2 * F)
+    xs = [randn(g, (M, 2 * F)) for _ in range(n)]
+    outs = [torch.empty(M, F, dtype=torch.bfloat16, device="cuda") for _ in range(n)]
+    L = _native.lib()
+
+    def step(i):
+        j = i % n
+        x = xs[j]
+        rc = L.qim_swiglu(x.data_ptr(), 2 * F, x.data_ptr() + F * 2, 2 * F, outs[j].data_ptr(), F, M, F,
+                          torch.cuda.current_stream().cuda_stream)
+        assert rc == 0
+    us = Timed(step, steps, warmup).run() * 1e3
+    return dict(kernel="qim_swiglu", us=us, bytes=nbytes, gbs=nbytes / us / 1e3,
+                frac=nbytes / us / 1e3 / HBM_PEAK_GBS, shape="[4352, 2x12288] -> [4352,12288]")
+
+
+def bench_residual(steps, warmup):
+    """Config 3b: gated residual of a [4352,3072] projection."""
+    from qwen_image_accel import _native
+    g = gen(91)
+    M, D = 4352, 3072
+    nbytes = 3 * M * D * 2 + D * 2
+    n = copies_for(2 * M * D * 2)
+    hs = [randn(g, (M, D)) for _ in range(n)]
+    xs = [randn(g, (M, D)) for _ in range(n)]
+    gate = randn(g, (1, D), 0.1)
+    outs = [torch.empty(M, D, dtype=torch.bfloat16, device="cuda") for _ in range(n)]
+    L = _native.lib()
+
+    def step(i):
+        j = i % n
+        rc = L.qim_gated_residual(hs[j].data_ptr(), xs[j].data_ptr(), gate.data_ptr(), outs[j].data_ptr(), M, D,
+                                  M, torch.cuda.current_stream().cuda_stream)
+        assert rc == 0
+    us = Timed(step, steps, warmup).run() * 1e3
+    return dict(kernel="qim_gated_residual", us=us, bytes=nbytes, gbs=nbytes / us / 1e3,
+                frac=nbytes / us / 1e3 / HBM_PEAK_GBS, shape="[4352,3072]")
+
+
+def bench_quantize(steps, warmup):
+    """Config 4a: MXFP8 activation quantize [4352,3072] with 1% outliers x20."""
+    from qwen_image_accel import _native
+    g = gen(0)
+    M, K = 4352, 3072
+    nbytes = 2 * M * K + M * K + M * K // 32
+    n = copies_for(2 * M * K)
+    xs = []
+    for _ in range(n):
+        a = torch.randn(M, K, generator=g)
+        a[torch.rand(M, K, generator=g) < 0.01] *= 20
+        xs.append(a.to(torch.bfloat16).cuda())
+    qs = [torch.empty(M, K, dtype=torch.uint8, device="cuda") for _ in range(n)]
+    ss = [torch.empty(M * K // 32, dtype=torch.uint8, device="cuda") for _ in range(n)]
+    L = _native.lib()
+
+    def step(i):
+        j = i % n
+        rc = L.qim_mx_quantize(xs[j].data_ptr(), K, M, K, qs[j].data_ptr(), ss[j].data_ptr(),
+                               torch.cuda.current_stream().cuda_stream)
+        assert rc == 0
+    us = Timed(step, steps, warmup).run() * 1e3
+    return dict(kernel="qim_mx_quantize", us=us, bytes=nbytes, gbs=nbytes / us / 1e3,
+                frac=nbytes / us / 1e3 / HBM_PEAK_GBS, shape="[4352,3072]")
+
+
+def bench_gemm(steps, warmup):
+    """Config 4b: MXFP8 GEMM [4352 x 3072] x [3072 x 12288] + bias."""
+    from qwen_image_accel import _native
+    from qwen_image_accel.kernels import mxfp8
+    g = gen(1)
+    M, K, N = 4352, 3072, 12288
+    a = torch.randn(M, K, generator=g)
+    a[torch.rand(M, K, generator=g) < 0.01] *= 20
+    aq = mxfp8.quantize(a.to(torch.bfloat16).cuda())
+    wq = mxfp8.quantize(randn(g, (N, K), 0.02))
+    bias = randn(g, (N,), 0.01)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    flops = 2 * M * N * K
+    L = _native.lib()
+
+    def step(i):
+        rc = L.qim_mxfp8_gemm(aq.values.data_ptr(), aq.scales.data_ptr(), wq.values.data_ptr(),
+                              wq.scales.data_ptr(), M, N, K, _native.EPI_BIAS, bias.data_ptr(), None, None,
+                              M, out.data_ptr(), N, None, torch.cuda.current_stream().cuda_stream)
+        assert rc == 0
+    us = Timed(step, max(10, steps // 4), warmup).run() * 1e3
+    tf = flops / us / 1e6
+    return dict(kernel="qim_mxfp8_gemm", us=us, flops=flops, tflops=tf, frac=tf / MXFP8_PEAK_TFLOPS,
+                shape="4352x3072x12288 +bias")
+
+
+def bench_block(tokens, steps, warmup):
+    """Config 5 / µs-per-block: one MMDiT block minus the attention core."""
+    from qwen_image_accel import rope
+    from qwen_image_accel.block import MMDiTBlock
+    g = gen(42)
+    blk = MMDiTBlock.random(g, device="cuda")
+    side = int(round(((tokens - 256)) ** 0.5))
+    h = randn(g, (1, tokens, 3072))
+    mod = randn(g, (1, 6, 3072), 0.1)
+    freqs = rope.image_table(256, side, side, "cuda")
+
+    def step(i):
+        blk.forward(h, mod, freqs)
+    us = Timed(step, max(3, steps // 20), warmup).run() * 1e3
+    flops = blk.flops(tokens)
+    return dict(us=us, flops=flops, tflops=flops / us / 1e6, tokens=tokens,
+                gemm_frac=flops / us / 1e6 / MXFP8_PEAK_TFLOPS)
+
+
+# ------------------------------------------------------------ CPU baseline --
+
+def cpu_baseline(seconds):
+    """The oracle's fused QK-RMSNorm + RoPE on the config-2 workload, repeated
+    until `seconds` of CPU time, on the host cores (OpenMP)."""
+    from oracle import oracle as O
+    threads = min(os.cpu_count() or 1, 16)
+    O.set_threads(threads)
+    rng = np.random.default_rng(721)
+    S, H, Dh = 4352, 24, 128
+    q = O.f32_to_bf16(rng.standard_normal((1, S, H, Dh), dtype=np.float32))
+    k = O.f32_to_bf16(rng.standard_normal((1, S, H, Dh), dtype=np.float32))
+    w = O.f32_to_bf16(rng.uniform(0.8, 1.2, Dh).astype(np.float32))
+    f = O.rope_freqs(O.rope_positions(256, 1, 64, 64))
+    nbytes = 4 * S * H * Dh * 2 + S * 64 * 8 + 2 * Dh * 2
+    O.norm_rope_pack(q, k, q, w, w, f)                      # warm-up
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        O.norm_rope_pack(q, k, q, w, w, f)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or reps >= 10000:
+            break
+    return {"value": nbytes * reps / el / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"config-2 workload (Q,K [1,4352,24,128]) x {reps} passes in {el:.1f} s, "
+                      f"C oracle, {threads} OpenMP threads"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--only", default="", help="comma list of components (debug)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(every hot-path op is token-row independent; see the sharding note in DESIGN.md).",
+              file=sys.stderr)
+        sys.exit(2)
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    from qwen_image_accel import _native
+    _native.lib()
+    only = set(filter(None, args.only.split(",")))
+
+    def want(name):
+        return not only or name in only
+
+    comp = {}
+    steps, warm = args.steps, args.warmup
+    for name, fn in [("qk_norm_rope_1024", lambda: bench_qk_norm_rope(steps, warm)),
+                     ("adaln_512", lambda: bench_adaln(steps, warm)),
+                     ("swiglu_1024", lambda: bench_swiglu(steps, warm)),
+                     ("gated_residual_1024", lambda: bench_residual(steps, warm)),
+                     ("quantize_1024", lambda: bench_quantize(steps, warm)),
+                     ("mxfp8_gemm_bias_1024", lambda: bench_gemm(steps, warm)),
+                     ("block_1024", lambda: bench_block(4352, steps, warm)),
+                     ("block_2048", lambda: bench_block(16640, steps, warm))]:
+        if not want(name):
+            continue
+        log(f"[bench] {name} ...")
+        comp[name] = fn()
+        log(f"[bench] {name}: {json.dumps(comp[name])}")
+        torch.cuda.empty_cache()
+
+    head = comp.get("qk_norm_rope_1024")
+    out = {
+        "metric": METRIC,
+        "value": round(head["gbs"], 1) if head else None,
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warm,
+        "ms_per_step": round(head["us"] / 1e3, 6) if head else None,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded randn; random-init weights ~N(0,0.02))",
+        "config": {"workload": "configs[1]: fused QK-RMSNorm + 3-axis RoPE @1024^2, Q,K bf16 [1,4352,24,128], "
+                               "eps 1e-6, theta 10000, dims 16/56/56, 256 text + 64x64 image tokens",
+                   "tokens": 4352, "heads": 24, "head_dim": 128},
+    }
+    if head:
+        out["roofline"] = {"bound": "hbm", "achieved": round(head["gbs"], 1), "peak": HBM_PEAK_GBS,
+                           "unit": "GB/s", "frac": round(head["frac"], 4), "traffic": None,
+                           "kernel": head["kernel"], "algorithmic_bytes": head["bytes"]}
+    summary = {}
+    for k, v in comp.items():
+        e = {"us": round(v["us"], 2)}
+        if "gbs" in v:
+            e.update(GBs=round(v["gbs"], 1), hbm_frac=round(v["frac"], 4))
+        if "tflops" in v:
+            e.update(TFLOPs=round(v["tflops"], 1), mfma_frac=round(v.get("frac", v.get("gemm_frac")), 4))
+        summary[k] = e
+    out["components"] = summary
+    if want("cpu"):
+        log("[bench] cpu baseline ...")
+        out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,157 @@
+/*
+ * qim.h -- C ABI of libqim.so, the MI355X (gfx950) kernels of the per-block
+ * transformer hot path of Qwen-Image-2.1-Accel.
+ *
+ * Every entry point takes raw device pointers, element counts and strides (in
+ * elements), and a hipStream_t passed as void* (NULL = the null stream).  It
+ * launches asynchronously on that stream and returns a qim_status; nothing is
+ * allocated, freed or synchronised, and no device state survives a call.
+ * bf16 tensors are uint16 bit patterns, E4M3 codes and E8M0 exponents are
+ * bytes, and MXFP8 scales use the 128x4 swizzled layout of the reference: the
+ * exponent of (row r, 32-element block kb) of a (rows, K) tensor lives at byte
+ *   ((r / 128) * (K / 128) + kb / 4) * 512 + (r % 32) * 16 + ((r % 128) / 32) * 4 + kb % 4
+ * (src/qwen_image_accel/kernels/mxfp8.py:53-56).  Quantized tensors are padded
+ * to Mp = ceil(M / 128) * 128 rows; padding rows hold code 0 and exponent 0.
+ *
+ * Each declaration names the reference interface it replaces (file:line under
+ * the reference tree src/qwen_image_accel/).
+ */
+#ifndef QIM_H
+#define QIM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum qim_status {
+    QIM_OK = 0,
+    QIM_ERR_ARG = 1,     /* null pointer or invalid argument value            */
+    QIM_ERR_SHAPE = 2,   /* shape the kernels do not support                  */
+    QIM_ERR_LAYOUT = 3,  /* stride or pointer alignment not supported         */
+    QIM_ERR_LAUNCH = 4,  /* the HIP runtime rejected the launch               */
+};
+
+/* Flags of qim_adaln / qim_adaln_quantize. */
+#define QIM_ADALN_ADD_ONE 1 /* use bf16(1 + scale) instead of scale */
+
+/* Epilogues of qim_mxfp8_gemm. */
+enum qim_epilogue {
+    QIM_EPI_NONE = 0,           /* out = bf16(acc)                                     */
+    QIM_EPI_BIAS = 1,           /* out = bf16(acc + bias[n])                           */
+    QIM_EPI_GATED_RESIDUAL = 2, /* out = bf16(res + bf16(gate[b, n] * bf16(acc)))      */
+    QIM_EPI_SWIGLU = 3,         /* out[m, j] = swiglu(bf16(acc_gate), bf16(acc_up))    */
+    QIM_EPI_SWIGLU_QUANT = 4,   /* MXFP8 codes + scales of the QIM_EPI_SWIGLU output   */
+};
+
+/* Rows of the gate and of the up projection alternate in groups of this many
+ * in a weight fed to the QIM_EPI_SWIGLU* epilogues: rows [2jG, 2jG+G) are gate
+ * rows [jG, jG+G) and rows [2jG+G, 2jG+2G) are up rows [jG, jG+G). */
+#define QIM_SWIGLU_GROUP 32
+
+/* Message of the last failing call on this host thread ("" if none). */
+const char *qim_last_error(void);
+
+/* ABI version of this header. */
+int qim_abi_version(void);
+
+/* quantize(x) -- src/qwen_image_accel/kernels/mxfp8.py:59-67 (kernel :30-56).
+ * x: bf16 (M, K), row stride ldx.  q: (Mp, K) E4M3 codes.  scales: Mp*K/32
+ * E8M0 bytes, swizzled.  K % 128 == 0, ldx % 8 == 0. */
+int qim_mx_quantize(const void *x, int64_t ldx, int64_t M, int64_t K,
+                    void *q, void *scales, void *stream);
+
+/* layer_norm_scale(x, scale, norm) -- src/qwen_image_accel/kernels/
+ * layernorm.py:58-86 (kernel :17-55), extended with the optional MMDiT shift,
+ * gate and residual: out = res + gate * (scale * LN(x) + shift) with a bf16
+ * rounding after each op.  x, res, out: (rows, D), rows = B * seq;
+ * scale, shift, gate: (B, D).  shift, gate, res may be NULL.  D % 8 == 0,
+ * D <= 8192. */
+int qim_adaln(const void *x, const void *scale, const void *shift, const void *gate,
+              const void *res, void *out, int64_t rows, int64_t D, int64_t seq,
+              float eps, int flags, void *stream);
+
+/* layer_norm_scale_quantize(x, scale, norm) -- src/qwen_image_accel/kernels/
+ * epilogue.py:145-161 (kernel :92-142): qim_adaln's output quantized to MXFP8
+ * instead of stored.  q: (Mp, D); scales: Mp*D/32.  D % 128 == 0. */
+int qim_adaln_quantize(const void *x, const void *scale, const void *shift, const void *gate,
+                       const void *res, void *q, void *scales, int64_t rows, int64_t D,
+                       int64_t seq, float eps, int flags, void *stream);
+
+/* residual(h, x, gate) -- src/qwen_image_accel/kernels/elementwise.py:26-34
+ * (kernel :10-23): out = bf16(h + bf16(gate * x)).  h, x, out: (rows, D);
+ * gate: (B, D), rows = B * seq.  D % 8 == 0. */
+int qim_gated_residual(const void *h, const void *x, const void *gate, void *out,
+                       int64_t rows, int64_t D, int64_t seq, void *stream);
+
+/* swiglu(gate, value) -- src/qwen_image_accel/kernels/bf16.py:27-36 (kernel
+ * :12-24): out = bf16(bf16(silu(g)) * v).  g, v, out: (M, F) with row strides
+ * ldg, ldv, ldo (strided halves of one (M, 2F) tensor are accepted).
+ * F % 8 == 0, strides % 8 == 0. */
+int qim_swiglu(const void *g, int64_t ldg, const void *v, int64_t ldv, void *out, int64_t ldo,
+               int64_t M, int64_t F, void *stream);
+
+/* swiglu_quantize(gate, value) -- src/qwen_image_accel/kernels/epilogue.py:
+ * 192-205 (kernel :164-189): swiglu quantized to MXFP8.  q: (Mp, F);
+ * scales: Mp*F/32.  F % 128 == 0. */
+int qim_swiglu_quantize(const void *g, int64_t ldg, const void *v, int64_t ldv,
+                        void *q, void *scales, int64_t M, int64_t F, void *stream);
+
+/* rms_norm(x, weight, eps) -- src/qwen_image_accel/kernels/bf16.py:58-63
+ * (kernel :46-55): out = bf16(bf16(x * rsqrt(mean(x^2) + eps)) * w) per row of
+ * D.  x, out: (rows, D); w: (D,).  D in {64, 128, 256}. */
+int qim_rms_norm(const void *x, const void *w, void *out, int64_t rows, int64_t D,
+                 float eps, void *stream);
+
+/* rope_qk(q, k, freqs) -- src/qwen_image_accel/kernels/elementwise.py:63-69
+ * (kernel :37-60).  q, k, oq, ok: (B, S, H, D) bf16; freqs: (S, D/2) complex64
+ * as interleaved fp32 (cos, sin).  D in {64, 128, 256}. */
+int qim_rope_qk(const void *q, const void *k, const void *freqs, void *oq, void *ok,
+                int64_t B, int64_t S, int64_t H, int64_t D, void *stream);
+
+/* prepare_attention_inputs(q, k, v, norm_q, norm_k, freqs, cached_k, cached_v)
+ * -- src/qwen_image_accel/kernels/attention.py:92-159 (kernel :16-89):
+ * oq = rope(RMSNorm_q(q)); ok = cat[ck, rope(RMSNorm_k(k))]; ov = cat[cv, v]
+ * along the sequence axis.  q, k, v: (B, S, H, D) with `ldt` elements between
+ * consecutive tokens (H*D when contiguous; 3*H*D for the Q/K/V column blocks
+ * of a fused QKV projection); oq: (B, S, H, D) contiguous; ck, cv: (B, P, H, D)
+ * (NULL when P == 0); ok, ov: (B, P+S, H, D); wq, wk: (D,) bf16.  v/ov may be
+ * NULL to skip the V pack (the fused QK-RMSNorm + RoPE of the MMDiT block).
+ * D in {64, 128, 256}. */
+int qim_qk_norm_rope_pack(const void *q, const void *k, const void *v, const void *ck,
+                          const void *cv, const void *wq, const void *wk, const void *freqs,
+                          void *oq, void *ok, void *ov, int64_t B, int64_t S, int64_t P,
+                          int64_t H, int64_t D, int64_t ldt, float epsq, float epsk,
+                          void *stream);
+
+/* MXFP8Linear.matmul(activation) -> torch._scaled_mm --
+ * src/qwen_image_accel/optimizations/mxfp8.py:32-36, with fused epilogues.
+ * aq: (Mp, K) E4M3 codes + as (swizzled over Mp rows); bq: (N, K) E4M3 codes of
+ * the weight (the reference's column-major (K, N) weight_fp8 view is these same
+ * bytes) + bs (swizzled over N rows).  fp32 accumulation.  Rows [0, M) are
+ * written.  out: bf16 (M, Nout) with row stride ldo, Nout = N (N/2 for the
+ * SWIGLU epilogues), or, for QIM_EPI_SWIGLU_QUANT, E4M3 codes (Mp, N/2) with
+ * out_scales (Mp*N/64 bytes, swizzled).  bias: (N,) bf16.  gate: (B, N) bf16,
+ * res: (M, N) bf16 (row stride N), B = ceil(M / seq).
+ * K % 128 == 0, N % 256 == 0 (N % 512 == 0 for the SWIGLU epilogues). */
+int qim_mxfp8_gemm(const void *aq, const void *as, const void *bq, const void *bs,
+                   int64_t M, int64_t N, int64_t K, int epilogue, const void *bias,
+                   const void *gate, const void *res, int64_t seq, void *out, int64_t ldo,
+                   void *out_scales, void *stream);
+
+/* Test hooks: the device conversions every kernel uses, applied elementwise
+ * (fp32 -> E4M3 code; fp32 -> bf16 bits), and one scaled MFMA
+ * (32x32x64, E4M3 x E4M3) on a single tile: a (32, 64) codes, b (32, 64) codes
+ * (row n of b is column n of the product), sa/sb (32, 2) E8M0 bytes,
+ * out (32, 32) fp32 = sum_k a*2^(sa-127) b*2^(sb-127). */
+int qim_debug_e4m3_encode(const float *x, void *codes, int64_t n, void *stream);
+int qim_debug_bf16_round(const float *x, void *bits, int64_t n, void *stream);
+int qim_debug_mfma_tile(const void *a, const void *b, const void *sa, const void *sb,
+                        float *out, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QIM_H */

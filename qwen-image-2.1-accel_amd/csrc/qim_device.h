@@ -1,0 +1,144 @@
+// Device helpers shared by every libqim kernel (gfx950 / CDNA4 only).
+//
+// bf16 values travel as uint16 bit patterns, packed two per dword; E4M3 codes
+// four per dword.  Conversions use the gfx950 hardware instructions
+// (v_cvt_pk_bf16_f32: round to nearest even; v_cvt_pk_fp8_f32: OCP E4M3, round
+// to nearest even); both are checked exhaustively against the CPU oracle
+// through qim_debug_bf16_round / qim_debug_e4m3_encode.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qim {
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------- bf16 ----
+
+__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+// Two fp32 -> packed bf16x2 (a in the low half), round to nearest even.
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+    f32x2_t v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
+// Eager ".to(bfloat16)" boundary: the fp32 value of the bf16 rounding of x.
+__device__ __forceinline__ float rbf(float x) { return bf_lo(pack_bf16x2(x, 0.0f)); }
+
+// Unpack 8 bf16 (one 16-byte vector) to fp32.
+__device__ __forceinline__ void unpack8(const uint4 &u, float *f) {
+    f[0] = bf_lo(u.x); f[1] = bf_hi(u.x); f[2] = bf_lo(u.y); f[3] = bf_hi(u.y);
+    f[4] = bf_lo(u.z); f[5] = bf_hi(u.z); f[6] = bf_lo(u.w); f[7] = bf_hi(u.w);
+}
+
+// Pack 8 fp32 to 8 bf16 (round to nearest even).
+__device__ __forceinline__ uint4 pack8(const float *f) {
+    uint4 u;
+    u.x = pack_bf16x2(f[0], f[1]); u.y = pack_bf16x2(f[2], f[3]);
+    u.z = pack_bf16x2(f[4], f[5]); u.w = pack_bf16x2(f[6], f[7]);
+    return u;
+}
+
+// ------------------------------------------------------------ MXFP8 ----
+
+// E8M0 exponent of a 32-element block with maximum |x| = amax: the smallest
+// power of two 2^(e-127) with amax / 2^(e-127) <= 448, read from the fp32 bits
+// (reference: src/qwen_image_accel/kernels/mxfp8.py:42-48).
+__device__ __forceinline__ int mx_exponent(float amax) {
+    uint32_t b = __float_as_uint(amax);
+    int e = (int)((b >> 23) & 0xffu) - 8 + ((b & 0x7fffffu) > 0x600000u ? 1 : 0);
+    e = e < 0 ? 0 : (e > 254 ? 254 : e);
+    return amax == 0.0f ? 0 : e;
+}
+
+// 2^(127 - e) as an exact fp32 bit pattern (kernels/mxfp8.py:49-51).
+__device__ __forceinline__ float mx_inverse(int e) { return __uint_as_float((uint32_t)(254 - e) << 23); }
+
+// Four fp32 -> four E4M3 codes packed little-endian in a dword.
+__device__ __forceinline__ uint32_t cvt_e4m3x4(float a, float b, float c, float d) {
+    int r = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    r = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, r, true);
+    return (uint32_t)r;
+}
+
+// Byte offset of the E8M0 exponent of (row r, block kb) of a (rows, K) tensor
+// in the 128x4 swizzled layout (kernels/mxfp8.py:53-56).
+__device__ __forceinline__ int64_t mx_scale_offset(int64_t r, int64_t kb, int64_t K) {
+    return ((r >> 7) * (K >> 7) + (kb >> 2)) * 512 + (r & 31) * 16 + ((r & 127) >> 5) * 4 + (kb & 3);
+}
+
+// |x| maximum of 8 values, as an fp32 bit pattern compared as unsigned
+// (monotonic for non-NaN values; no canonicalisation needed).
+__device__ __forceinline__ uint32_t absmax_bits8(const float *f) {
+    uint32_t m = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        uint32_t a = __float_as_uint(f[i]) & 0x7fffffffu;
+        m = a > m ? a : m;
+    }
+    return m;
+}
+
+// --------------------------------------------------------- shuffles ----
+
+// Lane exchange with lane ^ MASK inside the wave.  MASK 1, 2 use DPP quad
+// permutes; masks below 32 use ds_swizzle (bit mode); 32 uses ds_bpermute.
+template <int MASK>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
+    if constexpr (MASK == 1) {
+        return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);
+    } else if constexpr (MASK == 2) {
+        return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);
+    } else if constexpr (MASK < 32) {
+        return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, (MASK << 10) | 0x1F);
+    } else {
+        return (uint32_t)__shfl_xor((int)v, MASK, 64);
+    }
+}
+
+template <int MASK>
+__device__ __forceinline__ float xor_lane(float v) {
+    return __uint_as_float(xor_lane<MASK>(__float_as_uint(v)));
+}
+
+// Sum over groups of WIDTH consecutive lanes (WIDTH a power of two <= 64);
+// every lane of the group receives the total.
+template <int WIDTH>
+__device__ __forceinline__ float group_sum(float v) {
+    if constexpr (WIDTH >= 2) v += xor_lane<1>(v);
+    if constexpr (WIDTH >= 4) v += xor_lane<2>(v);
+    if constexpr (WIDTH >= 8) v += xor_lane<4>(v);
+    if constexpr (WIDTH >= 16) v += xor_lane<8>(v);
+    if constexpr (WIDTH >= 32) v += xor_lane<16>(v);
+    if constexpr (WIDTH >= 64) v += xor_lane<32>(v);
+    return v;
+}
+
+template <int WIDTH>
+__device__ __forceinline__ uint32_t group_umax(uint32_t v) {
+    uint32_t o;
+    if constexpr (WIDTH >= 2) { o = xor_lane<1>(v); v = o > v ? o : v; }
+    if constexpr (WIDTH >= 4) { o = xor_lane<2>(v); v = o > v ? o : v; }
+    if constexpr (WIDTH >= 8) { o = xor_lane<4>(v); v = o > v ? o : v; }
+    if constexpr (WIDTH >= 16) { o = xor_lane<8>(v); v = o > v ? o : v; }
+    if constexpr (WIDTH >= 32) { o = xor_lane<16>(v); v = o > v ? o : v; }
+    if constexpr (WIDTH >= 64) { o = xor_lane<32>(v); v = o > v ? o : v; }
+    return v;
+}
+
+// ------------------------------------------------------------- math ----
+
+// SiLU with the reference's rounding: bf16(g / (1 + exp(-g))) with an IEEE
+// (correctly rounded) fp32 divide -- the default for '/' in HIP without
+// fast-math -- and the device library's expf (kernels/bf16.py:17-22).
+__device__ __forceinline__ float silu_bf16(float g) { return rbf(g / (1.0f + expf(-g))); }
+
+// swiglu element: bf16(bf16(silu(g)) * v) with an fp32 multiply.
+__device__ __forceinline__ float swiglu1(float g, float v) { return rbf(silu_bf16(g) * v); }
+
+}  // namespace qim

@@ -1,0 +1,101 @@
+// Error state of the libqim C ABI and the test hooks of its device conversions.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "qim_device.h"
+#include "qim_runtime.h"
+
+namespace qim {
+
+static thread_local char g_error[512];
+
+int fail(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_error, sizeof(g_error), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int check_launch(const char *what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(QIM_ERR_LAUNCH, "%s: launch failed: %s", what, hipGetErrorString(e));
+    g_error[0] = '\0';
+    return QIM_OK;
+}
+
+// ----------------------------------------------------------- test hooks ----
+
+__global__ void k_debug_e4m3(const float *__restrict__ x, uint8_t *__restrict__ codes, int64_t n) {
+    int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    if (i + 4 <= n) {
+        uint32_t w = cvt_e4m3x4(x[i], x[i + 1], x[i + 2], x[i + 3]);
+        *reinterpret_cast<uint32_t *>(codes + i) = w;
+    } else {
+        for (int64_t j = i; j < n; ++j)
+            codes[j] = (uint8_t)(cvt_e4m3x4(x[j], 0.0f, 0.0f, 0.0f) & 0xffu);
+    }
+}
+
+__global__ void k_debug_bf16(const float *__restrict__ x, uint16_t *__restrict__ bits, int64_t n) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) bits[i] = (uint16_t)(pack_bf16x2(x[i], 0.0f) & 0xffffu);
+}
+
+// One v_mfma_scale_f32_32x32x64_f8f6f4 on a single tile.  Operand layout
+// (CDNA4): lane l holds row (l % 32) of A and column (l % 32) of B, K bytes
+// [32 * (l / 32), +32), and the E8M0 exponent of exactly those 32 values.
+// Result: lane l, register i holds D[8 * (i / 4) + 4 * (l / 32) + i % 4][l % 32].
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+__global__ void k_debug_mfma(const uint8_t *__restrict__ a, const uint8_t *__restrict__ b,
+                             const uint8_t *__restrict__ sa, const uint8_t *__restrict__ sb,
+                             float *__restrict__ out) {
+    const int l = threadIdx.x;
+    const int r = l & 31, kh = l >> 5;
+    i32x8_t av, bv;
+    const int *ap = reinterpret_cast<const int *>(a + r * 64 + kh * 32);
+    const int *bp = reinterpret_cast<const int *>(b + r * 64 + kh * 32);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) { av[i] = ap[i]; bv[i] = bp[i]; }
+    int sav = sa[r * 2 + kh], sbv = sb[r * 2 + kh];
+    f32x16_t acc = {};
+    acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bv, acc, 0, 0, 0, sav, 0, sbv);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) out[(8 * (i / 4) + 4 * kh + (i % 4)) * 32 + r] = acc[i];
+}
+
+}  // namespace qim
+
+using namespace qim;
+
+extern "C" const char *qim_last_error(void) { return g_error; }
+
+extern "C" int qim_abi_version(void) { return 1; }
+
+extern "C" int qim_debug_e4m3_encode(const float *x, void *codes, int64_t n, void *stream) {
+    QIM_REQUIRE(x && codes && n >= 0, QIM_ERR_ARG, "qim_debug_e4m3_encode: bad arguments");
+    if (n == 0) return QIM_OK;
+    int64_t threads = (n + 3) / 4;
+    hipLaunchKernelGGL(k_debug_e4m3, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                       as_stream(stream), x, (uint8_t *)codes, n);
+    return check_launch("qim_debug_e4m3_encode");
+}
+
+extern "C" int qim_debug_bf16_round(const float *x, void *bits, int64_t n, void *stream) {
+    QIM_REQUIRE(x && bits && n >= 0, QIM_ERR_ARG, "qim_debug_bf16_round: bad arguments");
+    if (n == 0) return QIM_OK;
+    hipLaunchKernelGGL(k_debug_bf16, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                       as_stream(stream), x, (uint16_t *)bits, n);
+    return check_launch("qim_debug_bf16_round");
+}
+
+extern "C" int qim_debug_mfma_tile(const void *a, const void *b, const void *sa, const void *sb,
+                                   float *out, void *stream) {
+    QIM_REQUIRE(a && b && sa && sb && out, QIM_ERR_ARG, "qim_debug_mfma_tile: null pointer");
+    QIM_REQUIRE(aligned16(a) && aligned16(b), QIM_ERR_LAYOUT, "qim_debug_mfma_tile: a, b must be 16-byte aligned");
+    hipLaunchKernelGGL(k_debug_mfma, dim3(1), dim3(64), 0, as_stream(stream), (const uint8_t *)a,
+                       (const uint8_t *)b, (const uint8_t *)sa, (const uint8_t *)sb, out);
+    return check_launch("qim_debug_mfma_tile");
+}

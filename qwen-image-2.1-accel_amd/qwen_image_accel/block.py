@@ -1,0 +1,116 @@
+"""One MMDiT transformer block on the MXFP8 path, minus the attention core.
+
+This is the block composition the reference's ``install_mx_fused_decode``
+installs (src/qwen_image_accel/optimizations/quantized_decode.py:108-137;
+eager definition WHL!diffusers/models/transformers/transformer_qwenimage21.py:
+615-649), in the MMDiT form of the benchmark configuration (shift + scale + gate
+modulation, fused QKV projection, hidden 3072, 24 heads x 128, FFN 12288):
+
+    x   = MXFP8(LN(h) * (1 + scale1) + shift1)             qim_adaln_quantize
+    qkv = x @ W_qkv                                         qim_mxfp8_gemm
+    q,k = rope(RMSNorm(q)), rope(RMSNorm(k))                qim_qk_norm_rope_pack
+    o   = attention(q, k, v)        -- out of scope; stand-in o = v
+    h   = h + tanh(g1) * (MXFP8(o) @ W_out)                 qim_mx_quantize + GEMM epilogue
+    x   = MXFP8(LN(h) * (1 + scale2) + shift2)             qim_adaln_quantize
+    a   = MXFP8(silu(x @ W_gate) * (x @ W_up))              GEMM, SwiGLU->MXFP8 epilogue
+    h   = h + tanh(g2) * (a @ W_down)                       GEMM, gated-residual epilogue
+
+Eight launches; every bf16 rounding point of the eager block is kept (the
+activation quantizations share one FP8 tensor per consumer group, as in
+quantized_decode.py:50-53, 81-96).  The modulation precompute (1 + s is done
+inside the LayerNorm kernel, tanh(g) in eager torch) is the reference's
+per-step precompute (optimizations/fusion.py:48-53).
+"""
+from dataclasses import dataclass
+
+import torch
+
+from qwen_image_accel.kernels import attention, gemm, mxfp8
+from qwen_image_accel.kernels.epilogue import layer_norm_scale_quantize
+
+
+class _LayerNorm:
+    """The block's affine-free LayerNorm (eps 1e-6) as the kernels' ``norm`` argument."""
+
+    def __init__(self, dim, eps=1e-6):
+        self.normalized_shape = (dim,)
+        self.eps = eps
+        self.elementwise_affine = False
+
+    def __call__(self, x):
+        return torch.nn.functional.layer_norm(x, self.normalized_shape, eps=self.eps)
+
+
+@dataclass
+class MMDiTBlock:
+    dim: int
+    heads: int
+    ffn: int
+    w_qkv: mxfp8.Quantized      # (3*dim, dim)
+    w_out: mxfp8.Quantized      # (dim, dim)
+    w_gate_up: mxfp8.Quantized  # (2*ffn, dim), gate/up rows interleaved
+    w_down: mxfp8.Quantized     # (dim, ffn)
+    norm_q: torch.Tensor        # (head_dim,) bf16
+    norm_k: torch.Tensor
+    bf16_weights: dict          # the unquantized bf16 weights (kept for checking)
+    eps: float = 1e-6
+
+    @staticmethod
+    def from_weights(w_qkv, w_out, w_gate, w_up, w_down, norm_q, norm_k, heads):
+        """Quantize bf16 weights once (like MXFP8Linear.__init__)."""
+        dim = w_out.shape[0]
+        ffn = w_gate.shape[0]
+        gu = gemm.interleave_swiglu(w_gate, w_up)
+        return MMDiTBlock(dim, heads, ffn, mxfp8.quantize(w_qkv), mxfp8.quantize(w_out),
+                          mxfp8.quantize(gu), mxfp8.quantize(w_down), norm_q, norm_k,
+                          dict(qkv=w_qkv, out=w_out, gate=w_gate, up=w_up, down=w_down,
+                               norm_q=norm_q, norm_k=norm_k))
+
+    @staticmethod
+    def random(gen, dim=3072, heads=24, ffn=12288, device="cuda", std=0.02):
+        """Random-init bf16 weights ~N(0, std^2) from a CPU generator."""
+        def w(*shape):
+            return (torch.randn(shape, generator=gen) * std).to(torch.bfloat16).to(device)
+        hd = dim // heads
+        nq = (torch.rand(hd, generator=gen) * 0.4 + 0.8).to(torch.bfloat16).to(device)
+        nk = (torch.rand(hd, generator=gen) * 0.4 + 0.8).to(torch.bfloat16).to(device)
+        return MMDiTBlock.from_weights(w(3 * dim, dim), w(dim, dim), w(ffn, dim), w(ffn, dim),
+                                       w(dim, ffn), nq, nk, heads)
+
+    def forward(self, h, modulation, freqs, attention_fn=None):
+        """h: (B, S, dim) bf16; modulation: (B, 6, dim) bf16 rows
+        (shift1, scale1, gate1, shift2, scale2, gate2); freqs: (S, head_dim/2)
+        complex64.  ``attention_fn(q, k, v) -> (B, S, dim)`` defaults to the
+        stand-in that returns v."""
+        b, s, d = h.shape
+        shift1, scale1, g1, shift2, scale2, g2 = (modulation[:, i:i + 1] for i in range(6))
+        gate1, gate2 = g1.tanh(), g2.tanh()
+        norm = _LayerNorm(d, self.eps)
+        hd = d // self.heads
+
+        x = layer_norm_scale_quantize(h, scale1.contiguous(), norm, shift=shift1.contiguous(),
+                                      add_one=True)
+        qkv = gemm.mx_matmul(x, self.w_qkv.values, self.w_qkv.scales)          # (B*S, 3d)
+        qkv4 = qkv.view(b, s, 3 * d)
+        q = qkv4[:, :, :d].unflatten(-1, (self.heads, hd))
+        k = qkv4[:, :, d:2 * d].unflatten(-1, (self.heads, hd))
+        q, k = attention.qk_norm_rope(q, k, self.norm_q, self.norm_k, freqs, self.eps, self.eps)
+        if attention_fn is None:
+            o = qkv[:, 2 * d:]                                                   # stand-in: v
+        else:
+            o = attention_fn(q, k, qkv4[:, :, 2 * d:].unflatten(-1, (self.heads, hd))).reshape(b * s, d)
+        oq = mxfp8.quantize(o)
+        h1 = gemm.mx_matmul(oq, self.w_out.values, self.w_out.scales, epilogue="gated_residual",
+                            gate=gate1.contiguous(), residual=h.reshape(b * s, d), seq=s)
+        h1 = h1.view(b, s, d)
+        x2 = layer_norm_scale_quantize(h1, scale2.contiguous(), norm, shift=shift2.contiguous(),
+                                       add_one=True)
+        a = gemm.mx_matmul(x2, self.w_gate_up.values, self.w_gate_up.scales, epilogue="swiglu_quant")
+        h2 = gemm.mx_matmul(a, self.w_down.values, self.w_down.scales, epilogue="gated_residual",
+                            gate=gate2.contiguous(), residual=h1.reshape(b * s, d), seq=s)
+        return h2.view(b, s, d)
+
+    def flops(self, tokens):
+        """GEMM flops of one forward over `tokens` rows (2*M*N*K each)."""
+        d, f = self.dim, self.ffn
+        return 2 * tokens * (3 * d * d + d * d + 2 * f * d + d * f)

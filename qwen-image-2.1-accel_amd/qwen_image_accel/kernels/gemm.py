@@ -1,0 +1,81 @@
+"""MXFP8 GEMM with fused epilogues (the ``torch._scaled_mm`` call site).
+
+Reference interface: src/qwen_image_accel/optimizations/mxfp8.py:32-36
+``MXFP8Linear.matmul`` = ``torch._scaled_mm(A_q, W_q, scale_a, scale_b,
+out_dtype=bf16)[:rows]``.  Here the product is libqim's ``qim_mxfp8_gemm``
+(CDNA4 scaled MFMA, fp32 accumulation) and the epilogue that follows the GEMM
+in the reference's block (bias, gated residual, SwiGLU, SwiGLU -> MXFP8) is
+applied before the store.
+"""
+import torch
+
+from qwen_image_accel import _native
+from qwen_image_accel.kernels.mxfp8 import Quantized, empty_quantized
+
+EPILOGUES = {
+    "none": _native.EPI_NONE,
+    "bias": _native.EPI_BIAS,
+    "gated_residual": _native.EPI_GATED_RESIDUAL,
+    "swiglu": _native.EPI_SWIGLU,
+    "swiglu_quant": _native.EPI_SWIGLU_QUANT,
+}
+
+
+def weight_rows(weight_fp8):
+    """The (N, K) row-major code matrix behind a weight given either as the
+    reference's column-major (K, N) ``values.t()`` view or as (N, K)."""
+    w = weight_fp8
+    if not w.is_contiguous() and w.t().is_contiguous():
+        w = w.t()
+    if not w.is_contiguous():
+        raise _native.Unsupported("mx_matmul", _native.QIM_ERR_LAYOUT, "weight codes must be dense")
+    return w
+
+
+def interleave_swiglu(gate_weight, up_weight, group=_native.SWIGLU_GROUP):
+    """Stack gate (F, K) and up (F, K) weights into the (2F, K) row order the
+    SwiGLU epilogues expect: groups of ``group`` gate rows, then the same up rows."""
+    f, k = gate_weight.shape
+    if up_weight.shape != (f, k) or f % group:
+        raise ValueError(f"gate/up weights must both be (F, K) with F % {group} == 0")
+    return torch.stack([gate_weight.reshape(f // group, group, k),
+                        up_weight.reshape(f // group, group, k)], dim=1).reshape(2 * f, k)
+
+
+def mx_matmul(activation, weight_fp8, weight_scale, *, epilogue="none", bias=None, gate=None,
+              residual=None, seq=None, out=None):
+    """``activation @ weight.T`` in MXFP8 with a fused epilogue.
+
+    activation: ``Quantized`` (Mp, K).  weight_fp8: codes of the (N, K) weight
+    (or its (K, N) column-major view); weight_scale: its swizzled scales.
+    Returns bf16 (rows, N) -- (rows, N/2) for "swiglu" -- or a ``Quantized``
+    (rows, N/2) for "swiglu_quant".  ``gate`` is (B, 1, N) or (B, N) with
+    ``seq`` rows per batch; ``residual`` is (rows, N)."""
+    epi = EPILOGUES[epilogue]
+    a = activation
+    w = weight_rows(weight_fp8)
+    n, k = w.shape
+    if a.values.shape[1] != k:
+        raise ValueError(f"activation K={a.values.shape[1]} does not match weight K={k}")
+    m = a.rows
+    dev = a.values.device
+    out_scales = None
+    if epi == _native.EPI_SWIGLU_QUANT:
+        result = empty_quantized(m, n // 2, dev)
+        buf, ldo, out_scales = result.values, n // 2, result.scales
+    else:
+        width = n // 2 if epi == _native.EPI_SWIGLU else n
+        if out is None:
+            out = torch.empty((m, width), device=dev, dtype=torch.bfloat16)
+        if out.dtype != torch.bfloat16 or out.stride(-1) != 1 or out.shape != (m, width):
+            raise ValueError("out must be a bf16 (rows, N) tensor with unit column stride")
+        buf, ldo, result = out, out.stride(0), out
+    if epi == _native.EPI_GATED_RESIDUAL:
+        gate = gate.reshape(-1, n)
+        if residual.shape != (m, n) or not residual.is_contiguous() or not gate.is_contiguous():
+            raise ValueError("gated residual needs a contiguous (rows, N) residual and (B, N) gate")
+    _native.call("qim_mxfp8_gemm", _native.ptr(a.values), _native.ptr(a.scales), _native.ptr(w),
+                 _native.ptr(weight_scale), m, n, k, epi, _native.ptr(bias), _native.ptr(gate),
+                 _native.ptr(residual), int(seq or m), _native.ptr(buf), ldo, _native.ptr(out_scales),
+                 _native.stream(dev))
+    return result

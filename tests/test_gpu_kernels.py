@@ -1,0 +1,414 @@
+"""Parity of the HIP kernels against the CPU oracle on identical seeded inputs.
+
+Bars: MXFP8 codes and E8M0 scales bit-exact; bf16
+ops within 1 bf16 ulp (or rel 4e-3) -- 2 ulps for a rare element of a chain
+whose intermediate bf16 rounding flips on a last-bit reduction difference;
+GEMM within rel-Frobenius 1e-2 of dequantize-then-matmul.
+Every test prints its case before the GPU step so a failing run names it.
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import oracle as O
+from qwen_image_accel import _native
+from qwen_image_accel.kernels import attention, bf16, elementwise, epilogue, gemm, layernorm, mxfp8
+from tests.helpers import (bf16_close, bf16_close_chain, bf16_randn, bf16_values, bits, from_bits,
+                           rel_fro)
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+def u8(t):
+    return t.view(torch.uint8).cpu().numpy()
+
+
+# ------------------------------------------------------------ conversions --
+
+def test_e4m3_hardware_conversion_exhaustive(dev):
+    """v_cvt_pk_fp8_f32 == oracle RNE on every finite bf16 value |v| < 448 and
+    on random fp32 values inside the range (the only inputs the quantizers
+    ever convert: block-scaled bf16 values)."""
+    v = bf16_values(np.arange(65536, dtype=np.uint16))
+    v = v[np.isfinite(v) & (np.abs(v) <= 448)]
+    rng = np.random.default_rng(0)
+    v = np.concatenate([v, rng.uniform(-448, 448, 200000).astype(np.float32)])
+    say("e4m3 exhaustive", v.size)
+    x = torch.from_numpy(v).to(dev)
+    out = torch.empty(v.size, dtype=torch.uint8, device=dev)
+    _native.call("qim_debug_e4m3_encode", _native.ptr(x), _native.ptr(out), v.size, _native.stream())
+    got = out.cpu().numpy()
+    ref = O.e4m3_encode(v)
+    bad = np.where(got != ref)[0]
+    assert bad.size == 0, [(float(v[i]), int(got[i]), int(ref[i])) for i in bad[:10]]
+
+
+def test_bf16_hardware_rounding(dev):
+    """v_cvt_pk_bf16_f32 == oracle RNE, subnormals included."""
+    rng = np.random.default_rng(1)
+    raw = rng.integers(0, 2 ** 32, 1 << 20, dtype=np.uint64).astype(np.uint32)
+    sub = rng.integers(0, 1 << 23, 1 << 16, dtype=np.uint64).astype(np.uint32)
+    v = np.concatenate([raw, sub, sub | 0x80000000]).view(np.float32)
+    v = v[np.isfinite(v)]
+    say("bf16 rounding", v.size)
+    x = torch.from_numpy(v).to(dev)
+    out = torch.empty(v.size, dtype=torch.int16, device=dev)
+    _native.call("qim_debug_bf16_round", _native.ptr(x), _native.ptr(out), v.size, _native.stream())
+    got = out.cpu().numpy().view(np.uint16)
+    ref = O.f32_to_bf16(v)
+    bad = np.where(got != ref)[0]
+    assert bad.size == 0, [(float(v[i]), hex(got[i]), hex(ref[i])) for i in bad[:10]]
+
+
+def test_scaled_mfma_lane_layout(dev):
+    """One v_mfma_scale_f32_32x32x64_f8f6f4 against the oracle product."""
+    rng = np.random.default_rng(2)
+    table = O.e4m3_values()
+    finite = np.where(np.isfinite(table))[0].astype(np.uint8)
+    a = rng.choice(finite, (32, 64))
+    b = rng.choice(finite, (32, 64))
+    sa = rng.integers(120, 135, (32, 2)).astype(np.uint8)
+    sb = rng.integers(120, 135, (32, 2)).astype(np.uint8)
+    ref = ((table[a] * np.exp2(np.repeat(sa.astype(np.float64), 32, 1) - 127)) @
+           (table[b] * np.exp2(np.repeat(sb.astype(np.float64), 32, 1) - 127)).T)
+    say("mfma tile")
+    t = [torch.from_numpy(np.ascontiguousarray(z)).to(dev) for z in (a, b, sa, sb)]
+    out = torch.zeros((32, 32), dtype=torch.float32, device=dev)
+    _native.call("qim_debug_mfma_tile", *[_native.ptr(z) for z in t], _native.ptr(out), _native.stream())
+    got = out.cpu().numpy()
+    assert np.allclose(got, ref, rtol=1e-5, atol=1e-6 * np.abs(ref).max()), np.abs(got - ref).max()
+
+
+# ---------------------------------------------------------------- quantize --
+
+@pytest.mark.parametrize("m,k", [(128, 4096), (1024, 4096), (1536, 4096), (2400, 4096), (4096, 12288),
+                                 (77, 4096), (1, 4096), (4352, 3072)])
+def test_quantize_bit_exact(dev, m, k):
+    """Shapes and outliers of the reference check (tests/gpu/check_mxfp8.py:38-50)."""
+    g = torch.Generator().manual_seed(0)
+    x = bf16_randn(g, (m, k))
+    x[:, ::512] *= 40
+    if m > 200:
+        x[m // 3] *= 1e-3
+    say("quantize", m, k)
+    a = mxfp8.quantize(x.to(dev))
+    q, s = O.mx_quantize(bits(x))
+    assert a.rows == m and a.values.shape == (mxfp8.padded_rows(m), k)
+    assert a.scales.dtype == torch.float8_e8m0fnu
+    assert np.array_equal(u8(a.values), q)
+    assert np.array_equal(u8(a.scales), s)
+
+
+def test_quantize_config4_outliers_and_strided_rows(dev):
+    """Config 4a input (1% outliers x20) read through a row stride."""
+    g = torch.Generator().manual_seed(0)
+    big = bf16_randn(g, (4352, 3072 + 64))
+    mask = torch.rand(big.shape, generator=g) < 0.01
+    big[mask] *= 20
+    x = big[:, 32:32 + 3072]
+    say("quantize strided", x.shape, x.stride())
+    a = mxfp8.quantize(x.to(dev))
+    q, s = O.mx_quantize(bits(x.contiguous()))
+    assert np.array_equal(u8(a.values), q) and np.array_equal(u8(a.scales), s)
+
+
+# ----------------------------------------------------------- LayerNorm --
+
+class _LN:
+    def __init__(self, d, eps=1e-6):
+        self.normalized_shape = (d,)
+        self.eps = eps
+        self.elementwise_affine = False
+
+    def __call__(self, x):
+        return F.layer_norm(x, self.normalized_shape, eps=self.eps)
+
+
+@pytest.mark.parametrize("b,n,d", [(1, 49, 4096), (2, 257, 4096), (1, 1024, 4096), (1, 1280, 3072),
+                                   (2, 33, 3072)])
+@pytest.mark.parametrize("mag", [0.001, 1.0, 20.0])
+def test_layer_norm_scale(dev, b, n, d, mag):
+    """Shapes and magnitudes of the reference check (check_layernorm_ops.py:13-22)."""
+    g = torch.Generator().manual_seed(717)
+    x = bf16_randn(g, (b, n, d), mag)
+    s = bf16_randn(g, (b, 1, d))
+    say("layer_norm_scale", b, n, d, mag)
+    before = _native.calls.get("qim_adaln", 0)
+    out = layernorm.layer_norm_scale(x.to(dev), s.to(dev), _LN(d))
+    assert _native.calls.get("qim_adaln", 0) == before + 1
+    ok, worst = bf16_close_chain(bits(out), O.adaln(bits(x), bits(s)))
+    assert ok, worst
+
+
+def test_adaln_config1_full_chain(dev):
+    """Config 1: out = res + gate * ((1 + scale) * LN(x) + shift) at 512^2."""
+    g = torch.Generator().manual_seed(717)
+    x = bf16_randn(g, (1, 1280, 3072))
+    shift, scale, gate = (bf16_randn(g, (1, 1, 3072), 0.1) for _ in range(3))
+    res = bf16_randn(g, (1, 1280, 3072))
+    say("adaln config1")
+    out = layernorm.layer_norm_scale(x.to(dev), scale.to(dev), _LN(3072), shift=shift.to(dev),
+                                     gate=gate.to(dev), residual=res.to(dev), add_one=True)
+    ref = O.adaln(bits(x), bits(scale), bits(shift), bits(gate), bits(res), add_one=True)
+    ok, worst = bf16_close_chain(bits(out), ref)
+    assert ok, worst
+
+
+@pytest.mark.parametrize("b,n,d", [(1, 1024, 4096), (1, 77, 4096), (2, 1024, 4096), (1, 4352, 3072),
+                                   (1, 130, 3072)])
+def test_layer_norm_scale_quantize(dev, b, n, d):
+    """Fused == quantize(separate) byte-for-byte (check_mx_epilogue.py:28-36)
+    and the codes agree with the oracle except where a last-bit LayerNorm
+    difference moved the bf16 value."""
+    g = torch.Generator().manual_seed(0)
+    x = bf16_randn(g, (b, n, d))
+    x[..., ::512] *= 25
+    s = bf16_randn(g, (b, 1, d))
+    say("layer_norm_scale_quantize", b, n, d)
+    xd, sd = x.to(dev), s.to(dev)
+    fused = epilogue.layer_norm_scale_quantize(xd, sd, _LN(d))
+    sep = mxfp8.quantize(layernorm.layer_norm_scale(xd, sd, _LN(d)).reshape(-1, d))
+    assert fused.rows == b * n and tuple(fused.shape) == (b, n, d)
+    assert np.array_equal(u8(fused.values), u8(sep.values))
+    assert np.array_equal(u8(fused.scales), u8(sep.scales))
+    q, sc = O.adaln_quantize(bits(x), bits(s))
+    assert (u8(fused.values) != q).mean() < 1e-3
+    assert (u8(fused.scales) != sc).mean() < 1e-3
+
+
+# --------------------------------------------------- residual, SwiGLU --
+
+@pytest.mark.parametrize("b,s,d", [(1, 49, 4096), (2, 257, 4096), (1, 4352, 3072)])
+def test_residual_bit_exact(dev, b, s, d):
+    g = torch.Generator().manual_seed(91)
+    h = bf16_randn(g, (b, s, d))
+    x = bf16_randn(g, (b, s, d))
+    gate = bf16_randn(g, (b, 1, d)).tanh()
+    say("residual", b, s, d)
+    out = elementwise.residual(h.to(dev), x.to(dev), gate.to(dev))
+    assert np.array_equal(bits(out), O.residual(bits(h), bits(x), bits(gate)))
+
+
+@pytest.mark.parametrize("m,f", [(1024, 12288), (128, 12288), (77, 256)])
+def test_swiglu(dev, m, f):
+    g = torch.Generator().manual_seed(91)
+    a = bf16_randn(g, (m, f), 2.0)
+    v = bf16_randn(g, (m, f))
+    say("swiglu", m, f)
+    out = bf16.swiglu(a.to(dev), v.to(dev))
+    ok, worst = bf16_close_chain(bits(out), O.swiglu(bits(a), bits(v)))
+    assert ok, worst
+
+
+def test_swiglu_strided_halves_config3(dev):
+    """Config 3: gate/up are the two halves of one (M, 2F) tensor."""
+    g = torch.Generator().manual_seed(91)
+    X = bf16_randn(g, (4352, 2 * 12288))
+    say("swiglu strided config3")
+    Xd = X.to(dev)
+    out = bf16.swiglu(Xd[:, :12288], Xd[:, 12288:])
+    assert _native.calls.get("qim_swiglu", 0) > 0
+    ok, worst = bf16_close_chain(bits(out), O.swiglu(bits(X[:, :12288]), bits(X[:, 12288:])))
+    assert ok, worst
+
+
+@pytest.mark.parametrize("rows,width", [(1024, 12288), (2400, 12288), (128, 12288), (77, 256)])
+def test_swiglu_quantize(dev, rows, width):
+    g = torch.Generator().manual_seed(0)
+    a = bf16_randn(g, (rows, width))
+    v = bf16_randn(g, (rows, width))
+    say("swiglu_quantize", rows, width)
+    ad, vd = a.to(dev), v.to(dev)
+    fused = epilogue.swiglu_quantize(ad, vd)
+    sep = mxfp8.quantize(bf16.swiglu(ad, vd))
+    assert np.array_equal(u8(fused.values), u8(sep.values))
+    assert np.array_equal(u8(fused.scales), u8(sep.scales))
+    q, s = O.swiglu_quantize(bits(a), bits(v))
+    assert (u8(fused.values) != q).mean() < 1e-3
+
+
+# ------------------------------------------------------ RMSNorm, RoPE --
+
+@pytest.mark.parametrize("mag", [0.001, 1.0, 20.0])
+def test_rms_norm(dev, mag):
+    g = torch.Generator().manual_seed(721)
+    x = bf16_randn(g, (1, 512, 24, 128), mag)
+    w = (torch.rand(128, generator=g) * 0.4 + 0.8).to(torch.bfloat16)
+    say("rms_norm", mag)
+    out = bf16.rms_norm(x.to(dev), w.to(dev), 1e-6)
+    ok, worst = bf16_close_chain(bits(out), O.rms_norm(bits(x), bits(w)))
+    assert ok, worst
+
+
+@pytest.mark.parametrize("b,s,h", [(1, 49, 32), (2, 257, 32), (1, 4096, 24)])
+def test_rope_qk_bit_exact(dev, b, s, h):
+    """Reference check shapes (check_fused.py:13-24), seed 91."""
+    g = torch.Generator().manual_seed(91)
+    q = bf16_randn(g, (b, s, h, 128))
+    k = bf16_randn(g, (b, s, h, 128))
+    phase = torch.randn(s, 64, generator=g)
+    freqs = torch.polar(torch.ones_like(phase), phase)
+    say("rope_qk", b, s, h)
+    oq, ok = elementwise.rope_qk(q.to(dev), k.to(dev), freqs.to(dev))
+    rq, rk = O.rope(bits(q), bits(k), torch.view_as_real(freqs).numpy())
+    assert np.array_equal(bits(oq), rq) and np.array_equal(bits(ok), rk)
+
+
+class _RMS:
+    def __init__(self, w, eps=1e-6):
+        self.weight, self.bias, self.eps = w, None, eps
+
+
+@pytest.mark.parametrize("b,s,p,h", [(1, 49, 0, 32), (2, 257, 7, 32), (1, 1024, 99, 32), (2, 49, 1024, 32),
+                                     (1, 300, 13, 24)])
+@pytest.mark.parametrize("mag", [0.001, 1.0, 20.0])
+def test_prepare_attention_inputs(dev, b, s, p, h, mag):
+    """Reference check shapes (check_attention_ops.py:13-31), seed 721."""
+    g = torch.Generator().manual_seed(721)
+    q = bf16_randn(g, (b, s, h, 128), mag)
+    k = bf16_randn(g, (b, s, h, 128), mag)
+    v = bf16_randn(g, (b, s, h, 128))
+    ck = bf16_randn(g, (b, p, h, 128))
+    cv = bf16_randn(g, (b, p, h, 128))
+    wq, wk = bf16_randn(g, (128,)), bf16_randn(g, (128,))
+    phase = torch.randn(s, 64, generator=g)
+    freqs = torch.polar(torch.ones_like(phase), phase)
+    say("prepare_attention_inputs", b, s, p, h, mag)
+    d = lambda t: t.to(dev)
+    oq, ok, ov = attention.prepare_attention_inputs(d(q), d(k), d(v), _RMS(d(wq)), _RMS(d(wk)), d(freqs),
+                                                    d(ck), d(cv))
+    rq, rk, rv = O.norm_rope_pack(bits(q), bits(k), bits(v), bits(wq), bits(wk),
+                                  torch.view_as_real(freqs).numpy(), bits(ck), bits(cv))
+    assert np.array_equal(bits(ov), rv)
+    assert np.array_equal(bits(ok)[:, :p], rk[:, :p])
+    for got, ref in ((bits(oq), rq), (bits(ok), rk)):
+        ok_, worst = bf16_close_chain(got, ref)
+        assert ok_, worst
+
+
+def test_prepare_attention_inputs_fallbacks(dev):
+    """None for unsupported inputs (check_attention_ops.py:37-41)."""
+    g = torch.Generator().manual_seed(721)
+    q = bf16_randn(g, (1, 16, 4, 128)).to(dev)
+    ck = bf16_randn(g, (1, 3, 4, 128)).to(dev)
+    w = _RMS(bf16_randn(g, (128,)).to(dev))
+    phase = torch.randn(16, 64, generator=g)
+    f = torch.polar(torch.ones_like(phase), phase).to(dev)
+    pai = attention.prepare_attention_inputs
+    assert pai(q, q, q, w, w, None, ck, ck) is None
+    assert pai(q.float(), q.float(), q.float(), w, w, f, ck, ck) is None
+    assert pai(q.transpose(1, 2), q.transpose(1, 2), q.transpose(1, 2), w, w, f, ck, ck) is None
+    assert pai(q, q, q, w, w, f, ck[:, :, :2], ck[:, :, :2]) is None
+
+
+def test_qk_norm_rope_config2_and_fused_qkv_view(dev):
+    """Config 2 at 1024^2 with the real 3-axis table; q/k read as column
+    blocks of a fused (S, 3*H*D) QKV output."""
+    S, H, D = 4352, 24, 128
+    g = torch.Generator().manual_seed(721)
+    qkv = bf16_randn(g, (S, 3 * H * D))
+    wq = (torch.rand(D, generator=g) * 0.4 + 0.8).to(torch.bfloat16)
+    wk = (torch.rand(D, generator=g) * 0.4 + 0.8).to(torch.bfloat16)
+    f = O.rope_freqs(O.rope_positions(256, 1, 64, 64))
+    freqs = torch.view_as_complex(torch.from_numpy(f))
+    say("qk_norm_rope config2")
+    qd = qkv.to(dev)
+    oq, ok = attention.qk_norm_rope(qd[:, :H * D], qd[:, H * D:2 * H * D], wq.to(dev), wk.to(dev),
+                                    freqs.to(dev), heads=H)
+    q = bits(qkv[:, :H * D].contiguous()).reshape(1, S, H, D)
+    k = bits(qkv[:, H * D:2 * H * D].contiguous()).reshape(1, S, H, D)
+    rq, rk, _ = O.norm_rope_pack(q, k, q, bits(wq), bits(wk), f)
+    for got, ref in ((bits(oq), rq), (bits(ok), rk)):
+        ok_, worst = bf16_close_chain(got, ref)
+        assert ok_, worst
+
+
+# ----------------------------------------------------------------- GEMM --
+
+def _quant_pair(g, m, n, k, wscale=0.02):
+    a = bf16_randn(g, (m, k))
+    w = bf16_randn(g, (n, k), wscale)
+    return a, w
+
+
+@pytest.mark.parametrize("m,n,k", [(256, 256, 128), (130, 512, 384), (1000, 768, 1024), (4352, 3072, 3072)])
+def test_mxfp8_gemm_plain(dev, m, n, k):
+    g = torch.Generator().manual_seed(1)
+    a, w = _quant_pair(g, m, n, k)
+    say("gemm", m, n, k)
+    aq = mxfp8.quantize(a.to(dev))
+    wq = mxfp8.quantize(w.to(dev))
+    y = gemm.mx_matmul(aq, wq.values, wq.scales)
+    assert y.shape == (m, n)
+    rows = np.arange(m) if m * n * k <= 1 << 31 else np.random.default_rng(0).choice(m, 64, replace=False)
+    ref = O.mx_gemm(u8(aq.values), u8(aq.scales), u8(wq.values), u8(wq.scales), rows=rows)
+    got = y.float().cpu().numpy()[rows]
+    assert rel_fro(got, ref) < 1e-2
+    # bf16 output of an fp32 accumulation: every element within 1 bf16 ulp + accumulation slack
+    assert np.all(np.abs(got - ref) <= 2.0 ** -7 * np.abs(ref) + 1e-3 * np.abs(ref).max())
+
+
+def test_mxfp8_gemm_bias_config4(dev):
+    """Config 4b: [4352 x 3072] x [3072 x 12288] + bias, sampled rows."""
+    g = torch.Generator().manual_seed(1)
+    a = bf16_randn(g, (4352, 3072))
+    mask = torch.rand(a.shape, generator=g) < 0.01
+    a[mask] *= 20
+    w = bf16_randn(g, (12288, 3072), 0.02)
+    bias = bf16_randn(g, (12288,), 0.01)
+    say("gemm bias config4")
+    aq = mxfp8.quantize(a.to(dev))
+    wq = mxfp8.quantize(w.to(dev))
+    y = gemm.mx_matmul(aq, wq.values.t(), wq.scales, epilogue="bias", bias=bias.to(dev))
+    rows = np.random.default_rng(0).choice(4352, 48, replace=False)
+    ref = O.mx_gemm(u8(aq.values), u8(aq.scales), u8(wq.values), u8(wq.scales), rows=rows)
+    ref = ref + bf16_values(bits(bias))[None, :]
+    assert rel_fro(y.float().cpu().numpy()[rows], ref) < 1e-2
+
+
+def test_mxfp8_gemm_gated_residual(dev):
+    g = torch.Generator().manual_seed(3)
+    m, n, k = 300, 512, 768
+    a, w = _quant_pair(g, m, n, k)
+    res = bf16_randn(g, (m, n))
+    gate = bf16_randn(g, (2, 1, n)).tanh()
+    say("gemm gated residual")
+    aq, wq = mxfp8.quantize(a.to(dev)), mxfp8.quantize(w.to(dev))
+    y = gemm.mx_matmul(aq, wq.values, wq.scales, epilogue="gated_residual", gate=gate.to(dev),
+                       residual=res.to(dev), seq=150)
+    acc = O.mx_gemm(u8(aq.values), u8(aq.scales), u8(wq.values), u8(wq.scales))[:m]
+    proj = O.f32_to_bf16(acc).reshape(2, 150, n)
+    ref = O.residual(bits(res).reshape(2, 150, n), proj, bits(gate))
+    # the GEMM output is within a bf16 ulp of the oracle's; the residual then adds it
+    got = bf16_values(bits(y)).reshape(2, 150, n)
+    assert rel_fro(got - bf16_values(bits(res)).reshape(2, 150, n),
+                   bf16_values(ref) - bf16_values(bits(res)).reshape(2, 150, n)) < 1e-2
+
+
+def test_mxfp8_gemm_swiglu_epilogues(dev):
+    g = torch.Generator().manual_seed(4)
+    m, f, k = 260, 512, 384
+    a = bf16_randn(g, (m, k))
+    wg = bf16_randn(g, (f, k), 0.05)
+    wu = bf16_randn(g, (f, k), 0.05)
+    say("gemm swiglu")
+    aq = mxfp8.quantize(a.to(dev))
+    wgu = gemm.interleave_swiglu(wg.to(dev), wu.to(dev))
+    wq = mxfp8.quantize(wgu)
+    y = gemm.mx_matmul(aq, wq.values, wq.scales, epilogue="swiglu")
+    yq = gemm.mx_matmul(aq, wq.values, wq.scales, epilogue="swiglu_quant")
+    acc = O.mx_gemm(u8(aq.values), u8(aq.scales), u8(wq.values), u8(wq.scales))[:m]
+    accg = acc.reshape(m, f // 32, 2, 32)[:, :, 0].reshape(m, f)
+    accu = acc.reshape(m, f // 32, 2, 32)[:, :, 1].reshape(m, f)
+    ref = O.swiglu(O.f32_to_bf16(accg), O.f32_to_bf16(accu))
+    assert y.shape == (m, f)
+    assert rel_fro(bf16_values(bits(y)), bf16_values(ref)) < 1e-2
+    # the quantized epilogue == quantize of the bf16 epilogue, byte for byte
+    sep = mxfp8.quantize(y)
+    assert yq.rows == m and np.array_equal(u8(yq.values), u8(sep.values))
+    assert np.array_equal(u8(yq.scales), u8(sep.scales))
