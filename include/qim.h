@@ -149,6 +149,9 @@ int qim_debug_e4m3_encode(const float *x, void *codes, int64_t n, void *stream);
 int qim_debug_bf16_round(const float *x, void *bits, int64_t n, void *stream);
 int qim_debug_mfma_tile(const void *a, const void *b, const void *sa, const void *sb,
                         float *out, void *stream);
+/* Scale-routing probe of the scaled MFMA (shape 0: 32x32x64, 1: 16x16x128):
+ * 4096 one-hot experiments, out: 4096 x 1024 (shape 0) or 4096 x 256 fp32. */
+int qim_debug_mfma_probe(int shape, float *out, void *stream);
 
 #ifdef __cplusplus
 }

@@ -4,9 +4,12 @@
 //
 // A: (Mp, K) E4M3 codes, B: (N, K) E4M3 codes (both K-contiguous), scales in
 // the 128x4 swizzled layout.  fp32 accumulation in v_mfma_scale_f32_32x32x64_
-// f8f6f4, which applies the E8M0 block scales inside the instruction: lane l
-// of a 32x32x64 step holds row l%32, K bytes [32(l/32), +32) of A (and the same
-// for a column of B), and the E8M0 exponent of exactly those 32 values.
+// f8f6f4, which applies the E8M0 block scales inside the instruction.  Lane l
+// of a 32x32x64 step holds row l%32 of A (column l%32 of B); with h = l/32 its
+// bytes 0-15 are K [16h, 16h+16) and bytes 16-31 are K [32+16h, 32+16h+16), so
+// bytes 0-15 of both half-waves form scale block 0 and bytes 16-31 block 1, and
+// lane l supplies the E8M0 exponent of (row l%32, block h).  (Measured with
+// qim_debug_mfma_probe: one-hot operands against per-lane exponents.)
 //
 // Workgroup tile 256 x 256, K step 128 bytes, 4 waves in a 2 x 2 grid, each
 // wave a 128 x 128 block of 4 x 4 MFMA tiles (256 fp32 accumulators per lane).
@@ -123,15 +126,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         }
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
-            const int c0 = kk * 4 + kh * 2;
+            const int clo = kk * 4 + kh, chi = kk * 4 + 2 + kh;  // 16-byte chunks of the 128-byte row
             i32x8_t av[4], bv[4];
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const int ra = wm * 128 + t * 32 + lr, rb = wn * 128 + t * 32 + lr;
-                const uint4 a0 = *reinterpret_cast<const uint4 *>(la + swz(ra, c0));
-                const uint4 a1 = *reinterpret_cast<const uint4 *>(la + swz(ra, c0 + 1));
-                const uint4 b0 = *reinterpret_cast<const uint4 *>(lb + swz(rb, c0));
-                const uint4 b1 = *reinterpret_cast<const uint4 *>(lb + swz(rb, c0 + 1));
+                const uint4 a0 = *reinterpret_cast<const uint4 *>(la + swz(ra, clo));
+                const uint4 a1 = *reinterpret_cast<const uint4 *>(la + swz(ra, chi));
+                const uint4 b0 = *reinterpret_cast<const uint4 *>(lb + swz(rb, clo));
+                const uint4 b1 = *reinterpret_cast<const uint4 *>(lb + swz(rb, chi));
                 av[t] = i32x8_t{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
                 bv[t] = i32x8_t{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
             }

@@ -43,8 +43,9 @@ __global__ void k_debug_bf16(const float *__restrict__ x, uint16_t *__restrict__
 }
 
 // One v_mfma_scale_f32_32x32x64_f8f6f4 on a single tile.  Operand layout
-// (CDNA4): lane l holds row (l % 32) of A and column (l % 32) of B, K bytes
-// [32 * (l / 32), +32), and the E8M0 exponent of exactly those 32 values.
+// (CDNA4): lane l holds row (l % 32) of A and column (l % 32) of B; with
+// h = l / 32 its bytes 0-15 are K [16h, +16) and bytes 16-31 are K [32 + 16h,
+// +16); lane l supplies the exponent of (row l % 32, K block h).
 // Result: lane l, register i holds D[8 * (i / 4) + 4 * (l / 32) + i % 4][l % 32].
 typedef int i32x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
@@ -55,10 +56,13 @@ __global__ void k_debug_mfma(const uint8_t *__restrict__ a, const uint8_t *__res
     const int l = threadIdx.x;
     const int r = l & 31, kh = l >> 5;
     i32x8_t av, bv;
-    const int *ap = reinterpret_cast<const int *>(a + r * 64 + kh * 32);
-    const int *bp = reinterpret_cast<const int *>(b + r * 64 + kh * 32);
+    const int *ap = reinterpret_cast<const int *>(a + r * 64 + kh * 16);
+    const int *bp = reinterpret_cast<const int *>(b + r * 64 + kh * 16);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) { av[i] = ap[i]; bv[i] = bp[i]; }
+    for (int i = 0; i < 4; ++i) {
+        av[i] = ap[i]; bv[i] = bp[i];            // K [16h, 16h + 16)
+        av[i + 4] = ap[i + 8]; bv[i + 4] = bp[i + 8];  // K [32 + 16h, +16)
+    }
     int sav = sa[r * 2 + kh], sbv = sb[r * 2 + kh];
     f32x16_t acc = {};
     acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bv, acc, 0, 0, 0, sav, 0, sbv);
@@ -66,9 +70,59 @@ __global__ void k_debug_mfma(const uint8_t *__restrict__ a, const uint8_t *__res
     for (int i = 0; i < 16; ++i) out[(8 * (i / 4) + 4 * kh + (i % 4)) * 32 + r] = acc[i];
 }
 
+// Scale-routing probe.  Experiment e = (operand, lane, byte): the probed
+// operand is one-hot (code 0x38 = 1.0 at that lane and byte), the other is all
+// ones; the probed operand's per-lane exponents are 100 + lane, the other's 127.
+// The output then holds 2^(lane' - 27) exactly at the row (A) or column (B) fed
+// by `lane`, where lane' is the lane whose exponent the hardware applied to
+// that byte.  SHAPE 0: 32x32x64 (out 32x32), 1: 16x16x128 (out 16x16).
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+template <int SHAPE>
+__global__ void k_debug_mfma_probe(float *__restrict__ out) {
+    const int e = blockIdx.x;               // 0 .. 4095
+    const int operand = e >> 11, plane = (e >> 5) & 63, pbyte = e & 31;
+    const int l = threadIdx.x;
+    i32x8_t one_hot, ones;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        ones[i] = 0x38383838;
+        int w = 0;
+        if (l == plane && (pbyte >> 2) == i) w = 0x38 << (8 * (pbyte & 3));
+        one_hot[i] = w;
+    }
+    const int s_probe = 100 + l, s_one = 127;
+    const i32x8_t a = operand == 0 ? one_hot : ones;
+    const i32x8_t b = operand == 0 ? ones : one_hot;
+    const int sa = operand == 0 ? s_probe : s_one;
+    const int sb = operand == 0 ? s_one : s_probe;
+    if constexpr (SHAPE == 0) {
+        f32x16_t acc = {};
+        acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, acc, 0, 0, 0, sa, 0, sb);
+        float *o = out + (size_t)e * 1024;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[(8 * (i / 4) + 4 * (l >> 5) + (i % 4)) * 32 + (l & 31)] = acc[i];
+    } else {
+        f32x4_t acc = {};
+        acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, acc, 0, 0, 0, sa, 0, sb);
+        float *o = out + (size_t)e * 256;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[(4 * (l >> 4) + i) * 16 + (l & 15)] = acc[i];
+    }
+}
+
 }  // namespace qim
 
 using namespace qim;
+
+extern "C" int qim_debug_mfma_probe(int shape, float *out, void *stream) {
+    QIM_REQUIRE(out && (shape == 0 || shape == 1), QIM_ERR_ARG, "qim_debug_mfma_probe: bad arguments");
+    if (shape == 0)
+        hipLaunchKernelGGL(k_debug_mfma_probe<0>, dim3(4096), dim3(64), 0, as_stream(stream), out);
+    else
+        hipLaunchKernelGGL(k_debug_mfma_probe<1>, dim3(4096), dim3(64), 0, as_stream(stream), out);
+    return check_launch("qim_debug_mfma_probe");
+}
 
 extern "C" const char *qim_last_error(void) { return g_error; }
 

@@ -57,6 +57,7 @@ SIGNATURES = {
     "qim_debug_e4m3_encode": (_C, [_P, _P, _I, _P]),
     "qim_debug_bf16_round": (_C, [_P, _P, _I, _P]),
     "qim_debug_mfma_tile": (_C, [_P, _P, _P, _P, _P, _P]),
+    "qim_debug_mfma_probe": (_C, [_C, _P, _P]),
 }
 
 _lib = None

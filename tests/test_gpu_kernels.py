@@ -74,14 +74,16 @@ def test_scaled_mfma_lane_layout(dev):
     b = rng.choice(finite, (32, 64))
     sa = rng.integers(120, 135, (32, 2)).astype(np.uint8)
     sb = rng.integers(120, 135, (32, 2)).astype(np.uint8)
-    ref = ((table[a] * np.exp2(np.repeat(sa.astype(np.float64), 32, 1) - 127)) @
-           (table[b] * np.exp2(np.repeat(sb.astype(np.float64), 32, 1) - 127)).T)
+    da = table[a] * np.exp2(np.repeat(sa.astype(np.float64), 32, 1) - 127)
+    db = table[b] * np.exp2(np.repeat(sb.astype(np.float64), 32, 1) - 127)
+    ref = da @ db.T
+    bound = 64 * 2.0 ** -24 * (np.abs(da) @ np.abs(db).T)  # fp32 accumulation of 64 exact products
     say("mfma tile")
     t = [torch.from_numpy(np.ascontiguousarray(z)).to(dev) for z in (a, b, sa, sb)]
     out = torch.zeros((32, 32), dtype=torch.float32, device=dev)
     _native.call("qim_debug_mfma_tile", *[_native.ptr(z) for z in t], _native.ptr(out), _native.stream())
     got = out.cpu().numpy()
-    assert np.allclose(got, ref, rtol=1e-5, atol=1e-6 * np.abs(ref).max()), np.abs(got - ref).max()
+    assert np.all(np.abs(got - ref) <= bound), np.max(np.abs(got - ref) / bound)
 
 
 # ---------------------------------------------------------------- quantize --
@@ -282,13 +284,27 @@ def test_prepare_attention_inputs(dev, b, s, p, h, mag):
     d = lambda t: t.to(dev)
     oq, ok, ov = attention.prepare_attention_inputs(d(q), d(k), d(v), _RMS(d(wq)), _RMS(d(wk)), d(freqs),
                                                     d(ck), d(cv))
-    rq, rk, rv = O.norm_rope_pack(bits(q), bits(k), bits(v), bits(wq), bits(wk),
-                                  torch.view_as_real(freqs).numpy(), bits(ck), bits(cv))
+    f = torch.view_as_real(freqs).numpy()
+    rq, rk, rv = O.norm_rope_pack(bits(q), bits(k), bits(v), bits(wq), bits(wk), f, bits(ck), bits(cv))
     assert np.array_equal(bits(ov), rv)
     assert np.array_equal(bits(ok)[:, :p], rk[:, :p])
-    for got, ref in ((bits(oq), rq), (bits(ok), rk)):
-        ok_, worst = bf16_close_chain(got, ref)
+    _check_norm_rope(dev, q, k, wq, wk, f, bits(oq), bits(ok)[:, p:])
+
+
+def _check_norm_rope(dev, q, k, wq, wk, f, got_q, got_k):
+    """Fused RMSNorm + RoPE == oracle RoPE of the GPU rms_norm output, bit for
+    bit (the fused kernel normalises with the rms_norm kernel's own reduction),
+    and the GPU rms_norm is within the bf16 chain tolerance of the oracle's.
+    RoPE cancellation makes a 1-ulp norm flip many ulps of a small output, so
+    the fused output is not compared with the oracle's ulp by ulp."""
+    nq = bf16.rms_norm(q.to(dev), wq.to(dev), 1e-6)
+    nk = bf16.rms_norm(k.to(dev), wk.to(dev), 1e-6)
+    for got, x, w in ((bits(nq), q, wq), (bits(nk), k, wk)):
+        ok_, worst = bf16_close_chain(got, O.rms_norm(bits(x), bits(w)))
         assert ok_, worst
+    rq, rk = O.rope(bits(nq), bits(nk), f)
+    assert np.array_equal(got_q, rq)
+    assert np.array_equal(got_k, rk)
 
 
 def test_prepare_attention_inputs_fallbacks(dev):
@@ -320,12 +336,9 @@ def test_qk_norm_rope_config2_and_fused_qkv_view(dev):
     qd = qkv.to(dev)
     oq, ok = attention.qk_norm_rope(qd[:, :H * D], qd[:, H * D:2 * H * D], wq.to(dev), wk.to(dev),
                                     freqs.to(dev), heads=H)
-    q = bits(qkv[:, :H * D].contiguous()).reshape(1, S, H, D)
-    k = bits(qkv[:, H * D:2 * H * D].contiguous()).reshape(1, S, H, D)
-    rq, rk, _ = O.norm_rope_pack(q, k, q, bits(wq), bits(wk), f)
-    for got, ref in ((bits(oq), rq), (bits(ok), rk)):
-        ok_, worst = bf16_close_chain(got, ref)
-        assert ok_, worst
+    q = qkv[:, :H * D].contiguous().reshape(1, S, H, D)
+    k = qkv[:, H * D:2 * H * D].contiguous().reshape(1, S, H, D)
+    _check_norm_rope(dev, q, k, wq, wk, f, bits(oq), bits(ok))
 
 
 # ----------------------------------------------------------------- GEMM --
