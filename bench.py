@@ -258,6 +258,21 @@ def bench_block(tokens, steps, warmup):
                 gemm_frac=flops / us / 1e6 / MXFP8_PEAK_TFLOPS)
 
 
+def bench_copy(steps, warmup):
+    """A plain device copy of 256 MiB: the achievable-bandwidth reference and
+    the calibration kernel of the FETCH_SIZE / WRITE_SIZE counters."""
+    n = 256 << 20
+    n_copies = copies_for(n)
+    src = [torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1) for _ in range(n_copies)]
+    dst = [torch.empty(n, dtype=torch.uint8, device="cuda") for _ in range(n_copies)]
+
+    def step(i):
+        dst[i % n_copies].copy_(src[i % n_copies])
+    us = Timed(step, max(10, steps // 10), warmup).run() * 1e3
+    return dict(kernel="copy", us=us, bytes=2 * n, gbs=2 * n / us / 1e3, frac=2 * n / us / 1e3 / HBM_PEAK_GBS,
+                shape="256 MiB")
+
+
 # ------------------------------------------------------------ CPU baseline --
 
 def cpu_baseline(seconds):
@@ -316,7 +331,8 @@ def main():
                      ("quantize_1024", lambda: bench_quantize(steps, warm)),
                      ("mxfp8_gemm_bias_1024", lambda: bench_gemm(steps, warm)),
                      ("block_1024", lambda: bench_block(4352, steps, warm)),
-                     ("block_2048", lambda: bench_block(16640, steps, warm))]:
+                     ("block_2048", lambda: bench_block(16640, steps, warm)),
+                     ("copy_256MiB", lambda: bench_copy(steps, warm))]:
         if not want(name):
             continue
         log(f"[bench] {name} ...")

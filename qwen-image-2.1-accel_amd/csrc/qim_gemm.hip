@@ -11,15 +11,19 @@
 // lane l supplies the E8M0 exponent of (row l%32, block h).  (Measured with
 // qim_debug_mfma_probe: one-hot operands against per-lane exponents.)
 //
-// Workgroup tile 256 x 256, K step 128 bytes, 4 waves in a 2 x 2 grid, each
-// wave a 128 x 128 block of 4 x 4 MFMA tiles (256 fp32 accumulators per lane).
-// A, B and their scale chunks go global -> registers -> LDS with double
-// buffering: the loads of stage s+1 are in flight while stage s computes.
-// LDS rows are 128 bytes; the 16-byte chunk c of row r is stored at chunk
-// c ^ ((r >> 1) & 7), so 16 lanes reading 16 consecutive rows at one chunk
-// touch 16 distinct (bank-half, chunk) slots.  The 512-byte scale chunk of a
-// (128 rows x 128 K) tile is copied verbatim, and a lane reads the dword of
-// its row, which holds the 4 exponents of the stage.
+// Workgroup tile 256 x 256, 4 waves in a 2 x 2 grid, each wave a 128 x 128
+// block of 4 x 4 MFMA tiles (256 fp32 accumulators per lane, in AGPRs).
+// K advances 64 bytes per stage through a 4-deep LDS ring (34 KiB per stage:
+// A 256 x 64, B 256 x 64, and the 1 KiB A / B scale chunks of the stage's
+// 128-K group).  Operands move global -> LDS with global_load_lds_dwordx4
+// (no register staging): lane i of an instruction writes LDS bytes
+// [16i, 16i+16) of a 1 KiB segment, so the bank swizzle is applied to the
+// source address instead -- LDS holds logical 16-byte chunk c of tile row r at
+// chunk c ^ (((r >> 1) ^ (r >> 2)) & 3), which makes 8 (and 16) lanes reading
+// 8 (16) consecutive rows at one chunk hit distinct banks.  Stage s+4 is
+// issued at the top of stage s, right after the barrier that proves every wave
+// has consumed ring slot s % 4; the fragments of stage s+1 are read from LDS
+// while the 16 MFMAs of stage s run.
 #include "qim_device.h"
 #include "qim_runtime.h"
 
@@ -27,12 +31,15 @@ namespace qim {
 
 typedef int i32x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void gbl_void_t;
 
-constexpr int BM = 256, BN = 256, BK = 128;
-constexpr int TILE_BYTES = BM * BK;          // 32 KiB per operand per stage
-constexpr int SCALE_BYTES = BM / 128 * 512;  // 1 KiB per operand per stage
-constexpr int STAGE_BYTES = 2 * TILE_BYTES + 2 * SCALE_BYTES;
-constexpr int LDS_BYTES = 2 * STAGE_BYTES;   // 132 KiB
+constexpr int BM = 256, BN = 256, BK = 64, NSTAGE = 4;
+constexpr int TILE_BYTES = BM * BK;                          // 16 KiB per operand per stage
+constexpr int SCALE_BYTES = 1024;                            // two 512-byte chunks per operand
+constexpr int STAGE_BYTES = 2 * TILE_BYTES + 2 * SCALE_BYTES;  // 34 KiB
+constexpr int LDS_BYTES = NSTAGE * STAGE_BYTES;              // 136 KiB
+constexpr int LOADS_PER_STAGE = 10;                          // per wave: 4 A + 4 B (16 B) + 2 scale (4 B)
 
 struct GemmArgs {
     const uint8_t *aq, *as, *bq, *bs;
@@ -42,64 +49,191 @@ struct GemmArgs {
     void *out;
     int64_t ldo;
     uint8_t *out_scales;
-    int tiles_n;
+    int tiles_m, tiles_n;
 };
 
-__device__ __forceinline__ int swz(int row, int chunk) { return row * BK + ((chunk ^ ((row >> 1) & 7)) << 4); }
-
-// Global -> register staging of one K stage.
-struct Stage {
-    uint4 a[8], b[8];
-    uint4 sc;  // threads 0..63: A scale piece; 64..127: B scale piece
-};
-
-__device__ __forceinline__ void load_stage(const GemmArgs &p, int64_t m0, int64_t n0, int s, Stage &st) {
-    const int tid = threadIdx.x;
-    const int64_t kofs = (int64_t)s * BK;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int ch = tid + 256 * i, row = ch >> 3, c = ch & 7;
-        const int64_t ar = m0 + row;
-        st.a[i] = ar < p.Mp ? *reinterpret_cast<const uint4 *>(p.aq + ar * p.K + kofs + c * 16) : make_uint4(0, 0, 0, 0);
-        st.b[i] = *reinterpret_cast<const uint4 *>(p.bq + (n0 + row) * p.K + kofs + c * 16);
-    }
-    const int kt = p.K / BK;
-    if (tid < 64) {
-        const int g = tid >> 5, piece = tid & 31;  // 128-row group, 16-byte piece of its 512-byte chunk
-        const int64_t grow = m0 / 128 + g;
-        st.sc = grow * 128 < p.Mp
-                    ? reinterpret_cast<const uint4 *>(p.as + (grow * kt + s) * 512)[piece]
-                    : make_uint4(0, 0, 0, 0);
-    } else if (tid < 128) {
-        const int g = (tid - 64) >> 5, piece = tid & 31;
-        const int64_t grow = n0 / 128 + g;
-        st.sc = reinterpret_cast<const uint4 *>(p.bs + (grow * kt + s) * 512)[piece];
-    }
-}
-
-__device__ __forceinline__ void store_stage(uint8_t *lds, const Stage &st) {
-    const int tid = threadIdx.x;
-    uint8_t *la = lds, *lb = lds + TILE_BYTES;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int ch = tid + 256 * i, row = ch >> 3, c = ch & 7;
-        *reinterpret_cast<uint4 *>(la + swz(row, c)) = st.a[i];
-        *reinterpret_cast<uint4 *>(lb + swz(row, c)) = st.b[i];
-    }
-    if (tid < 128) reinterpret_cast<uint4 *>(lds + 2 * TILE_BYTES)[tid] = st.sc;
-}
-
+__device__ __forceinline__ int kswz(int row) { return ((row >> 1) ^ (row >> 2)) & 3; }
+// LDS byte offset of logical 16-byte chunk c of tile row `row` (64-byte rows).
+__device__ __forceinline__ int lds_off(int row, int c) { return row * BK + ((c ^ kswz(row)) << 4); }
 // Offset of the scale dword of local row r (0..255) inside a 1 KiB scale tile.
 __device__ __forceinline__ int scale_dword(int r) { return (r >> 7) * 512 + (r & 31) * 16 + ((r & 127) >> 5) * 4; }
 
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N < 64, "vmcnt is 6 bits");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ void block_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// Per-lane source offsets of the 10 load instructions of a stage (stage 0);
+// stage s adds s * 64 (operands) or (s / 2) * 512 (scales).
+struct LoadPlan {
+    uint32_t a[4], b[4];      // byte offsets into aq / bq
+    uint32_t sc[2];           // byte offsets into as (idx < 4) or bs
+    bool sc_is_b[2];
+    int wave;
+};
+
+__device__ __forceinline__ LoadPlan make_plan(const GemmArgs &p, int64_t m0, int64_t n0) {
+    LoadPlan L;
+    const int lane = threadIdx.x & 63;
+    L.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int row = (L.wave * 4 + j) * 16 + (lane >> 2);
+        const int c = (lane & 3) ^ kswz(row);
+        int64_t ar = m0 + row;
+        ar = ar < p.Mp ? ar : p.Mp - 1;  // rows past Mp only feed output rows that are never stored
+        L.a[j] = (uint32_t)(ar * p.K + c * 16);
+        L.b[j] = (uint32_t)((n0 + row) * p.K + c * 16);
+    }
+    const int64_t kt = p.K / 128;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int idx = L.wave * 2 + j;          // 0..3: A scale quarter, 4..7: B scale quarter
+        const int off = (idx & 3) * 256 + lane * 4;
+        const int g = off >> 9, o = off & 511;
+        L.sc_is_b[j] = idx >= 4;
+        int64_t grow;
+        if (idx < 4) {
+            grow = m0 / 128 + g;
+            grow = grow < p.Mp / 128 ? grow : p.Mp / 128 - 1;
+        } else {
+            grow = n0 / 128 + g;
+        }
+        L.sc[j] = (uint32_t)(grow * kt * 512 + o);
+    }
+    return L;
+}
+
+// LDS DMA through inline asm: the compiler does not see these as LDS writes,
+// so it does not force vmcnt(0) before every LDS read (it cannot prove the
+// ring slots disjoint); the ring's own vmcnt waits and s_barrier order them.
+// M0 holds the wave-uniform LDS destination; lane i lands at M0 + 16i (4i for
+// the dword form).  M0 is set inside the statement, right before its use.
+__device__ __forceinline__ void dma16(const uint8_t *base, uint32_t voff, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base),
+                 "s"(lds_addr)
+                 : "memory");
+}
+__device__ __forceinline__ void dma4(const uint8_t *base, uint32_t voff, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(base),
+                 "s"(lds_addr)
+                 : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const uint8_t *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)p;
+}
+
+__device__ __forceinline__ void issue_stage(const GemmArgs &p, const LoadPlan &L, uint8_t *slot, int s) {
+    const uint32_t kofs = (uint32_t)s * BK;
+    const uint32_t base = lds_addr(slot);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dma16(p.aq, L.a[j] + kofs, base + (L.wave * 4 + j) * 1024);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dma16(p.bq, L.b[j] + kofs, base + TILE_BYTES + (L.wave * 4 + j) * 1024);
+    const uint32_t gofs = (uint32_t)(s >> 1) * 512;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+        dma4(L.sc_is_b[j] ? p.bs : p.as, L.sc[j] + gofs, base + 2 * TILE_BYTES + (L.wave * 2 + j) * 256);
+}
+
+struct Frags {
+    i32x8_t a[4], b[4];
+    uint32_t sa[4], sb[4];
+};
+
+// Read one stage's MFMA operands.  Scale dwords of the upper half-wave are
+// shifted by one byte so that byte (s % 2) * 2 is this lane's block for every
+// lane and the MFMA can select it with a uniform op_sel.
+__device__ __forceinline__ void read_frags(const uint8_t *slot, int wm, int wn, int lr, int kh, Frags &f) {
+    const uint8_t *la = slot, *lb = slot + TILE_BYTES;
+    const uint8_t *lsa = slot + 2 * TILE_BYTES, *lsb = lsa + SCALE_BYTES;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const int ra = wm * 128 + t * 32 + lr, rb = wn * 128 + t * 32 + lr;
+        const uint4 a0 = *reinterpret_cast<const uint4 *>(la + lds_off(ra, kh));
+        const uint4 a1 = *reinterpret_cast<const uint4 *>(la + lds_off(ra, 2 + kh));
+        const uint4 b0 = *reinterpret_cast<const uint4 *>(lb + lds_off(rb, kh));
+        const uint4 b1 = *reinterpret_cast<const uint4 *>(lb + lds_off(rb, 2 + kh));
+        f.a[t] = i32x8_t{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+        f.b[t] = i32x8_t{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+        f.sa[t] = *reinterpret_cast<const uint32_t *>(lsa + scale_dword(ra));
+        f.sb[t] = *reinterpret_cast<const uint32_t *>(lsb + scale_dword(rb));
+    }
+}
+
+// The scale dwords hold the exponents of K blocks 0..3 of the stage's 128-K
+// group; the upper half-wave's are shifted down one byte so that byte
+// (s % 2) * 2 is every lane's own block and op_sel can select it uniformly.
+template <int PAR>
+__device__ __forceinline__ void mma_stage(f32x16_t (&acc)[4][4], const Frags &f, int kh) {
+    int sa[4], sb[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        sa[t] = (int)(f.sa[t] >> (8 * kh));
+        sb[t] = (int)(f.sb[t] >> (8 * kh));
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.a[i], f.b[j], acc[i][j], 0, 0, PAR * 2,
+                                                                        sa[i], PAR * 2, sb[j]);
+}
+
+// Wait until this wave's loads of stage s + 1 have landed, given that the
+// stages issued so far end at min(s + 3, S - 1).  (At the last stage nothing
+// is outstanding and the wait is a no-op.)
+__device__ __forceinline__ void wait_next(int s, int S) {
+    const int after = S - 2 - s;  // stages issued after s + 1
+    if (after >= 2) wait_vmcnt<2 * LOADS_PER_STAGE>();
+    else if (after == 1) wait_vmcnt<LOADS_PER_STAGE>();
+    else wait_vmcnt<0>();
+}
+
+// One pipeline step: stage s (parity PAR) is in `cur`; stage s+1 is read
+// into `nxt` while the MFMAs of stage s run.
+template <int PAR>
+__device__ __forceinline__ void pipeline_step(const GemmArgs &p, const LoadPlan &L, uint8_t *lds, int s, int S,
+                                              f32x16_t (&acc)[4][4], const Frags &cur, Frags &nxt, int wm,
+                                              int wn, int lr, int kh) {
+    wait_next(s, S);
+    block_barrier();
+    if (s + 4 < S) issue_stage(p, L, lds + (s & 3) * STAGE_BYTES, s + 4);
+    // At the last stage this reads a stale slot; the values are never used.
+    read_frags(lds + ((s + 1) & 3) * STAGE_BYTES, wm, wn, lr, kh, nxt);
+    mma_stage<PAR>(acc, cur, kh);
+}
+
+// Workgroup -> tile.  Workgroups are dispatched round-robin over the 8 XCDs,
+// so workgroup w runs on XCD w % 8; tile ids are remapped so that each XCD
+// owns one contiguous range, walked in groups of 4 tile-rows (column-major
+// inside a group) so the tiles resident on one XCD share A rows and B columns
+// in that XCD's L2.
+__device__ __forceinline__ void tile_of(const GemmArgs &p, int &tm, int &tn) {
+    const int nt = p.tiles_m * p.tiles_n;
+    int t = blockIdx.x;
+    if ((nt & 7) == 0) t = (t & 7) * (nt >> 3) + (t >> 3);
+    constexpr int GM = 4;
+    const int per_group = GM * p.tiles_n;
+    const int group = t / per_group, first = group * GM;
+    const int gm = p.tiles_m - first < GM ? p.tiles_m - first : GM;
+    const int r = t - group * per_group;
+    tm = first + r % gm;
+    tn = r / gm;
+}
+
 template <int EPI>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_mx_gemm(GemmArgs p) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
-    const int tm = blockIdx.x / p.tiles_n, tn = blockIdx.x % p.tiles_n;
+    int tm, tn;
+    tile_of(p, tm, tn);
     const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
-    const int stages = (int)(p.K / BK);
+    const int S = (int)(p.K / BK);
     const int lr = lane & 31, kh = lane >> 5;
 
     f32x16_t acc[4][4];
@@ -108,50 +242,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
 
-    Stage st;
-    load_stage(p, m0, n0, 0, st);
-    store_stage(lds, st);
-    __syncthreads();
+    const LoadPlan L = make_plan(p, m0, n0);
+#pragma unroll
+    for (int i = 0; i < NSTAGE; ++i)
+        if (i < S) issue_stage(p, L, lds + i * STAGE_BYTES, i);
+    // Stage 0 landed: at most min(S, 4) - 1 later stages still outstanding.
+    if (S >= 4) wait_vmcnt<3 * LOADS_PER_STAGE>();
+    else if (S == 3) wait_vmcnt<2 * LOADS_PER_STAGE>();
+    else if (S == 2) wait_vmcnt<LOADS_PER_STAGE>();
+    else wait_vmcnt<0>();
+    block_barrier();
+    Frags fa, fb;
+    read_frags(lds, wm, wn, lr, kh, fa);
 
-    for (int s = 0; s < stages; ++s) {
-        uint8_t *cur = lds + (s & 1) * STAGE_BYTES;
-        if (s + 1 < stages) load_stage(p, m0, n0, s + 1, st);
-        const uint8_t *la = cur, *lb = cur + TILE_BYTES;
-        const uint8_t *lsa = cur + 2 * TILE_BYTES, *lsb = lsa + SCALE_BYTES;
-        uint32_t sa[4], sb[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            sa[t] = *reinterpret_cast<const uint32_t *>(lsa + scale_dword(wm * 128 + t * 32 + lr));
-            sb[t] = *reinterpret_cast<const uint32_t *>(lsb + scale_dword(wn * 128 + t * 32 + lr));
-        }
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-            const int clo = kk * 4 + kh, chi = kk * 4 + 2 + kh;  // 16-byte chunks of the 128-byte row
-            i32x8_t av[4], bv[4];
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const int ra = wm * 128 + t * 32 + lr, rb = wn * 128 + t * 32 + lr;
-                const uint4 a0 = *reinterpret_cast<const uint4 *>(la + swz(ra, clo));
-                const uint4 a1 = *reinterpret_cast<const uint4 *>(la + swz(ra, chi));
-                const uint4 b0 = *reinterpret_cast<const uint4 *>(lb + swz(rb, clo));
-                const uint4 b1 = *reinterpret_cast<const uint4 *>(lb + swz(rb, chi));
-                av[t] = i32x8_t{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
-                bv[t] = i32x8_t{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
-            }
-            const int shift = (kk * 2 + kh) * 8;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int ea = (int)((sa[i] >> shift) & 0xffu);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int eb = (int)((sb[j] >> shift) & 0xffu);
-                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av[i], bv[j], acc[i][j], 0, 0, 0, ea,
-                                                                                0, eb);
-                }
-            }
-        }
-        if (s + 1 < stages) store_stage(lds + ((s + 1) & 1) * STAGE_BYTES, st);
-        __syncthreads();
+    // S = K / 64 is even (K % 128 == 0): stages come in (even, odd) pairs.
+    for (int s = 0; s < S; s += 2) {
+        pipeline_step<0>(p, L, lds, s, S, acc, fa, fb, wm, wn, lr, kh);
+        pipeline_step<1>(p, L, lds, s + 1, S, acc, fb, fa, wm, wn, lr, kh);
     }
 
     // ------------------------------------------------------------ epilogue
@@ -238,16 +345,18 @@ extern "C" int qim_mxfp8_gemm(const void *aq, const void *as, const void *bq, co
                               int64_t seq, void *out, int64_t ldo, void *out_scales, void *stream) {
     QIM_REQUIRE(aq && as && bq && bs && out, QIM_ERR_ARG, "qim_mxfp8_gemm: null pointer");
     QIM_REQUIRE(M > 0 && N > 0 && K > 0, QIM_ERR_SHAPE, "qim_mxfp8_gemm: empty problem");
-    QIM_REQUIRE(K % BK == 0, QIM_ERR_SHAPE, "qim_mxfp8_gemm: K=%lld is not a multiple of 128", (long long)K);
+    QIM_REQUIRE(K % 128 == 0, QIM_ERR_SHAPE, "qim_mxfp8_gemm: K=%lld is not a multiple of 128", (long long)K);
     QIM_REQUIRE(N % BN == 0, QIM_ERR_SHAPE, "qim_mxfp8_gemm: N=%lld is not a multiple of 256", (long long)N);
     const int64_t Mp = (M + 127) / 128 * 128;
     const int64_t tiles_m = (Mp + BM - 1) / BM, tiles_n = N / BN;
     QIM_REQUIRE(tiles_m * tiles_n < (1ll << 31), QIM_ERR_SHAPE, "qim_mxfp8_gemm: too many tiles");
     QIM_REQUIRE(aligned16(aq) && aligned16(bq) && aligned16(as) && aligned16(bs), QIM_ERR_LAYOUT,
                 "qim_mxfp8_gemm: operands must be 16-byte aligned");
+    QIM_REQUIRE(Mp * K < (1ll << 31) && N * K < (1ll << 31), QIM_ERR_SHAPE,
+                "qim_mxfp8_gemm: operands above 2 GiB are not supported");
     GemmArgs a{(const uint8_t *)aq, (const uint8_t *)as, (const uint8_t *)bq, (const uint8_t *)bs, M, Mp, N, K,
                (const uint16_t *)bias, (const uint16_t *)gate, (const uint16_t *)res, seq > 0 ? seq : M, out, ldo,
-               (uint8_t *)out_scales, (int)tiles_n};
+               (uint8_t *)out_scales, (int)tiles_m, (int)tiles_n};
     const int64_t tiles = tiles_m * tiles_n;
     int rc;
     switch (epilogue) {
