@@ -52,7 +52,10 @@ def build(verbose=False):
         if verbose and msgs.strip():
             print(msgs)
     tmp = OUT + ".tmp"
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *[o for o, _ in results]]
+    # -Bsymbolic: the library's own references (kernel stubs, helpers) bind
+    # inside it, never to a same-named symbol of another loaded library.
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-Bsymbolic", "-o", tmp,
+           *[o for o, _ in results]]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}{r.stderr}")

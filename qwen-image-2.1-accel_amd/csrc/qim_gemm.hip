@@ -69,8 +69,8 @@ __device__ __forceinline__ void block_barrier() { asm volatile("s_barrier" ::: "
 // stage s adds s * 64 (operands) or (s / 2) * 512 (scales).
 struct LoadPlan {
     uint32_t a[4], b[4];      // byte offsets into aq / bq
-    uint32_t sc[2];           // byte offsets into as (idx < 4) or bs
-    bool sc_is_b[2];
+    uint32_t sc[2];           // byte offsets into sc_base
+    const uint8_t *sc_base[2];  // as (A scale quarter) or bs (B scale quarter); wave-uniform
     int wave;
 };
 
@@ -93,7 +93,7 @@ __device__ __forceinline__ LoadPlan make_plan(const GemmArgs &p, int64_t m0, int
         const int idx = L.wave * 2 + j;          // 0..3: A scale quarter, 4..7: B scale quarter
         const int off = (idx & 3) * 256 + lane * 4;
         const int g = off >> 9, o = off & 511;
-        L.sc_is_b[j] = idx >= 4;
+        L.sc_base[j] = idx >= 4 ? p.bs : p.as;
         int64_t grow;
         if (idx < 4) {
             grow = m0 / 128 + g;
@@ -136,7 +136,7 @@ __device__ __forceinline__ void issue_stage(const GemmArgs &p, const LoadPlan &L
     const uint32_t gofs = (uint32_t)(s >> 1) * 512;
 #pragma unroll
     for (int j = 0; j < 2; ++j)
-        dma4(L.sc_is_b[j] ? p.bs : p.as, L.sc[j] + gofs, base + 2 * TILE_BYTES + (L.wave * 2 + j) * 256);
+        dma4(L.sc_base[j], L.sc[j] + gofs, base + 2 * TILE_BYTES + (L.wave * 2 + j) * 256);
 }
 
 struct Frags {
@@ -144,67 +144,102 @@ struct Frags {
     uint32_t sa[4], sb[4];
 };
 
-// Read one stage's MFMA operands.  Scale dwords of the upper half-wave are
-// shifted by one byte so that byte (s % 2) * 2 is this lane's block for every
-// lane and the MFMA can select it with a uniform op_sel.
+// Fragment reads of one ring slot (stage), one operand tile at a time.
+__device__ __forceinline__ i32x8_t read_tile(const uint8_t *base, int row, int kh) {
+    const uint4 lo = *reinterpret_cast<const uint4 *>(base + lds_off(row, kh));
+    const uint4 hi = *reinterpret_cast<const uint4 *>(base + lds_off(row, 2 + kh));
+    return i32x8_t{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+}
+__device__ __forceinline__ uint32_t read_scale(const uint8_t *base, int row) {
+    return *reinterpret_cast<const uint32_t *>(base + scale_dword(row));
+}
+
 __device__ __forceinline__ void read_frags(const uint8_t *slot, int wm, int wn, int lr, int kh, Frags &f) {
-    const uint8_t *la = slot, *lb = slot + TILE_BYTES;
-    const uint8_t *lsa = slot + 2 * TILE_BYTES, *lsb = lsa + SCALE_BYTES;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-        const int ra = wm * 128 + t * 32 + lr, rb = wn * 128 + t * 32 + lr;
-        const uint4 a0 = *reinterpret_cast<const uint4 *>(la + lds_off(ra, kh));
-        const uint4 a1 = *reinterpret_cast<const uint4 *>(la + lds_off(ra, 2 + kh));
-        const uint4 b0 = *reinterpret_cast<const uint4 *>(lb + lds_off(rb, kh));
-        const uint4 b1 = *reinterpret_cast<const uint4 *>(lb + lds_off(rb, 2 + kh));
-        f.a[t] = i32x8_t{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
-        f.b[t] = i32x8_t{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
-        f.sa[t] = *reinterpret_cast<const uint32_t *>(lsa + scale_dword(ra));
-        f.sb[t] = *reinterpret_cast<const uint32_t *>(lsb + scale_dword(rb));
+        f.a[t] = read_tile(slot, wm * 128 + t * 32 + lr, kh);
+        f.b[t] = read_tile(slot + TILE_BYTES, wn * 128 + t * 32 + lr, kh);
+        f.sa[t] = read_scale(slot + 2 * TILE_BYTES, wm * 128 + t * 32 + lr);
+        f.sb[t] = read_scale(slot + 2 * TILE_BYTES + SCALE_BYTES, wn * 128 + t * 32 + lr);
     }
 }
 
+// Every stage issues its 10 loads unconditionally (past the end of K they
+// re-read the last stage into a ring slot that is never read again), so at
+// the top of stage s the outstanding loads are always those of stages s+1,
+// s+2, s+3, and "stage s+1 landed" is always vmcnt(20).  Keeping the stage
+// free of branches keeps it one basic block, which the explicit schedule
+// below needs.
+
+#define QIM_SCHED() __builtin_amdgcn_sched_barrier(0)
+
+// One pipeline step with an explicit instruction order (the scheduler may not
+// move anything across QIM_SCHED()).  With one wave per SIMD the MFMA pipe
+// idles whenever the wave stalls, so the 16 MFMAs of stage s (operands in
+// `cur`) are spread around everything else the stage has to do:
+//   MFMA 0 | wait for stage s+1's DMA, barrier | MFMA 1-3, each followed by a
+//   third of the 10 DMA issues of stage s+4 | MFMA 4-15, each followed by two
+//   of the 24 LDS reads of stage s+1's operands into `nxt`.
 // The scale dwords hold the exponents of K blocks 0..3 of the stage's 128-K
 // group; the upper half-wave's are shifted down one byte so that byte
 // (s % 2) * 2 is every lane's own block and op_sel can select it uniformly.
 template <int PAR>
-__device__ __forceinline__ void mma_stage(f32x16_t (&acc)[4][4], const Frags &f, int kh) {
-    int sa[4], sb[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        sa[t] = (int)(f.sa[t] >> (8 * kh));
-        sb[t] = (int)(f.sb[t] >> (8 * kh));
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.a[i], f.b[j], acc[i][j], 0, 0, PAR * 2,
-                                                                        sa[i], PAR * 2, sb[j]);
-}
-
-// Wait until this wave's loads of stage s + 1 have landed, given that the
-// stages issued so far end at min(s + 3, S - 1).  (At the last stage nothing
-// is outstanding and the wait is a no-op.)
-__device__ __forceinline__ void wait_next(int s, int S) {
-    const int after = S - 2 - s;  // stages issued after s + 1
-    if (after >= 2) wait_vmcnt<2 * LOADS_PER_STAGE>();
-    else if (after == 1) wait_vmcnt<LOADS_PER_STAGE>();
-    else wait_vmcnt<0>();
-}
-
-// One pipeline step: stage s (parity PAR) is in `cur`; stage s+1 is read
-// into `nxt` while the MFMAs of stage s run.
-template <int PAR>
 __device__ __forceinline__ void pipeline_step(const GemmArgs &p, const LoadPlan &L, uint8_t *lds, int s, int S,
                                               f32x16_t (&acc)[4][4], const Frags &cur, Frags &nxt, int wm,
                                               int wn, int lr, int kh) {
-    wait_next(s, S);
+    int sa[4], sb[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        sa[t] = (int)(cur.sa[t] >> (8 * kh));
+        sb[t] = (int)(cur.sb[t] >> (8 * kh));
+    }
+#define QIM_MF(i, j)                                                                                          \
+    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(cur.a[i], cur.b[j], acc[i][j], 0, 0, PAR * 2, \
+                                                                sa[i], PAR * 2, sb[j])
+    uint8_t *fill = lds + (s & 3) * STAGE_BYTES;
+    const uint8_t *next = lds + ((s + 1) & 3) * STAGE_BYTES;  // stale at the last stage; unused then
+    const int sl = s + 4 < S ? s + 4 : S - 1;                 // stage to load (clamped)
+    const uint32_t kofs = (uint32_t)sl * BK, gofs = (uint32_t)(sl >> 1) * 512;
+    const uint32_t fb = lds_addr(fill);
+    const int ra0 = wm * 128 + lr, rb0 = wn * 128 + lr;
+
+    const uint8_t *nsa = next + 2 * TILE_BYTES, *nsb = nsa + SCALE_BYTES;
+    const uint8_t *scb0 = L.sc_base[0], *scb1 = L.sc_base[1];
+    const uint32_t w4 = L.wave * 4;
+#define QIM_STEP(mi, mj, work) QIM_MF(mi, mj); QIM_SCHED(); work; QIM_SCHED()
+    QIM_MF(0, 0);
+    QIM_SCHED();
+    wait_vmcnt<2 * LOADS_PER_STAGE>();
     block_barrier();
-    if (s + 4 < S) issue_stage(p, L, lds + (s & 3) * STAGE_BYTES, s + 4);
-    // At the last stage this reads a stale slot; the values are never used.
-    read_frags(lds + ((s + 1) & 3) * STAGE_BYTES, wm, wn, lr, kh, nxt);
-    mma_stage<PAR>(acc, cur, kh);
+    QIM_SCHED();
+    QIM_STEP(0, 1, dma16(p.aq, L.a[0] + kofs, fb + (w4 + 0) * 1024));
+    QIM_STEP(0, 2, dma16(p.aq, L.a[1] + kofs, fb + (w4 + 1) * 1024);
+             nxt.sa[0] = read_scale(nsa, ra0); nxt.sa[1] = read_scale(nsa, ra0 + 32);
+             nxt.sa[2] = read_scale(nsa, ra0 + 64); nxt.sa[3] = read_scale(nsa, ra0 + 96));
+    QIM_STEP(0, 3, dma16(p.aq, L.a[2] + kofs, fb + (w4 + 2) * 1024);
+             nxt.sb[0] = read_scale(nsb, rb0); nxt.sb[1] = read_scale(nsb, rb0 + 32);
+             nxt.sb[2] = read_scale(nsb, rb0 + 64); nxt.sb[3] = read_scale(nsb, rb0 + 96));
+    QIM_STEP(1, 0, dma16(p.aq, L.a[3] + kofs, fb + (w4 + 3) * 1024); nxt.a[0] = read_tile(next, ra0, kh));
+    QIM_STEP(1, 1, dma16(p.bq, L.b[0] + kofs, fb + TILE_BYTES + (w4 + 0) * 1024);
+             nxt.b[0] = read_tile(next + TILE_BYTES, rb0, kh));
+    QIM_STEP(1, 2, dma16(p.bq, L.b[1] + kofs, fb + TILE_BYTES + (w4 + 1) * 1024);
+             nxt.b[1] = read_tile(next + TILE_BYTES, rb0 + 32, kh));
+    QIM_STEP(1, 3, dma16(p.bq, L.b[2] + kofs, fb + TILE_BYTES + (w4 + 2) * 1024);
+             nxt.b[2] = read_tile(next + TILE_BYTES, rb0 + 64, kh));
+    QIM_STEP(2, 0, dma16(p.bq, L.b[3] + kofs, fb + TILE_BYTES + (w4 + 3) * 1024);
+             nxt.b[3] = read_tile(next + TILE_BYTES, rb0 + 96, kh));
+    QIM_STEP(2, 1, dma4(scb0, L.sc[0] + gofs, fb + 2 * TILE_BYTES + (L.wave * 2 + 0) * 256);
+             nxt.a[1] = read_tile(next, ra0 + 32, kh));
+    QIM_STEP(2, 2, dma4(scb1, L.sc[1] + gofs, fb + 2 * TILE_BYTES + (L.wave * 2 + 1) * 256);
+             nxt.a[2] = read_tile(next, ra0 + 64, kh));
+    QIM_STEP(2, 3, nxt.a[3] = read_tile(next, ra0 + 96, kh));
+    QIM_MF(3, 0);
+    QIM_MF(3, 1);
+    QIM_MF(3, 2);
+    QIM_MF(3, 3);
+    QIM_SCHED();
+#undef QIM_STEP
+#undef QIM_MF
 }
 
 // Workgroup -> tile.  Workgroups are dispatched round-robin over the 8 XCDs,
@@ -223,6 +258,105 @@ __device__ __forceinline__ void tile_of(const GemmArgs &p, int &tm, int &tn) {
     const int r = t - group * per_group;
     tm = first + r % gm;
     tn = r / gm;
+}
+
+// ------------------------------------------------------------- epilogue --
+// Two passes per half of the wave's 128 rows, through a wave-private LDS
+// region (the ring is free once the main loop has drained):
+//  1. registers -> LDS: each accumulator goes through the per-element part of
+//     the epilogue (bias add, or SwiGLU of the gate/up tile pair) and is
+//     stored as bf16 at its (row, column);
+//  2. LDS -> global: each lane reads 8 consecutive bf16 of a row (16 bytes)
+//     and applies the per-row part (gated residual with coalesced res/gate
+//     loads, or MXFP8 quantization of 32-column blocks = 4 lanes) before one
+//     16-byte (8-byte for codes) store.
+// Accumulator i of MFMA tile (ti, tj) is row 32ti + 8(i/4) + 4(l/32) + i%4,
+// column 32tj + l%32 of the wave's block.  Row stride 2W + 16 bytes (W = 128
+// or 64 output columns) keeps both passes free of bank conflicts.
+template <int EPI>
+__device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[4][4], uint8_t *lds, int wm, int wn,
+                                         int64_t m0, int64_t n0, int lane) {
+    constexpr bool SWI = EPI == QIM_EPI_SWIGLU || EPI == QIM_EPI_SWIGLU_QUANT;
+    constexpr int W = SWI ? 64 : 128;        // output columns of this wave
+    constexpr int RS = 2 * W + 16;           // LDS row stride (bytes)
+    constexpr int LPR = W / 8;               // lanes per row in pass 2
+    constexpr int RPI = 64 / LPR;            // rows per pass-2 instruction
+    const int lr = lane & 31, kh = lane >> 5;
+    const int wave = threadIdx.x >> 6;
+    uint8_t *reg = lds + wave * (64 * RS);
+    const int64_t row0 = m0 + wm * 128;
+    const int64_t col0 = SWI ? (n0 + wn * 128) / 2 : n0 + wn * 128;  // first output column
+    const int64_t F = p.N / 2;
+    float bias[4] = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (EPI == QIM_EPI_BIAS) {
+#pragma unroll
+        for (int tj = 0; tj < 4; ++tj) bias[tj] = bf16_to_f32(p.bias[n0 + wn * 128 + tj * 32 + lr]);
+    }
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+        // pass 1
+#pragma unroll
+        for (int tl = 0; tl < 2; ++tl) {
+            const int ti = half * 2 + tl;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int r = tl * 32 + 8 * (i >> 2) + 4 * kh + (i & 3);
+                uint16_t *rowp = reinterpret_cast<uint16_t *>(reg + r * RS);
+                if constexpr (SWI) {
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        const float y = swiglu1(rbf(acc[ti][2 * u][i]), rbf(acc[ti][2 * u + 1][i]));
+                        rowp[u * 32 + lr] = (uint16_t)(pack_bf16x2(y, 0.0f) & 0xffffu);
+                    }
+                } else {
+#pragma unroll
+                    for (int tj = 0; tj < 4; ++tj) {
+                        float v = acc[ti][tj][i];
+                        if constexpr (EPI == QIM_EPI_BIAS) v = v + bias[tj];
+                        rowp[tj * 32 + lr] = (uint16_t)(pack_bf16x2(v, 0.0f) & 0xffffu);
+                    }
+                }
+            }
+        }
+        // pass 2 (LDS operations of one wave complete in order: no wait needed)
+        const int cl = lane % LPR, rl = lane / LPR;
+#pragma unroll
+        for (int it = 0; it < 64 / RPI; ++it) {
+            const int r = it * RPI + rl;
+            const int64_t grow = row0 + half * 64 + r;
+            const int64_t col = col0 + cl * 8;
+            const uint4 v = *reinterpret_cast<const uint4 *>(reg + r * RS + cl * 16);
+            if constexpr (EPI == QIM_EPI_SWIGLU_QUANT) {
+                float f[8];
+                unpack8(v, f);
+                const uint32_t m = group_umax<4>(absmax_bits8(f));
+                const int e = mx_exponent(__uint_as_float(m));
+                const float inv = mx_inverse(e);
+                uint2 c;
+                c.x = cvt_e4m3x4(f[0] * inv, f[1] * inv, f[2] * inv, f[3] * inv);
+                c.y = cvt_e4m3x4(f[4] * inv, f[5] * inv, f[6] * inv, f[7] * inv);
+                if (grow < p.Mp) {
+                    *reinterpret_cast<uint2 *>(reinterpret_cast<uint8_t *>(p.out) + grow * F + col) = c;
+                    if ((cl & 3) == 0) p.out_scales[mx_scale_offset(grow, col >> 5, F)] = (uint8_t)e;
+                }
+            } else {
+                if (grow >= p.M) continue;
+                uint4 o = v;
+                if constexpr (EPI == QIM_EPI_GATED_RESIDUAL) {
+                    const uint4 hv = *reinterpret_cast<const uint4 *>(p.res + grow * p.N + col);
+                    const uint4 gv = *reinterpret_cast<const uint4 *>(p.gate + (grow / p.seq) * p.N + col);
+                    float y[8], h[8], g[8], z[8];
+                    unpack8(v, y);
+                    unpack8(hv, h);
+                    unpack8(gv, g);
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) z[t] = h[t] + rbf(g[t] * y[t]);
+                    o = pack8(z);
+                }
+                *reinterpret_cast<uint4 *>(reinterpret_cast<uint16_t *>(p.out) + grow * p.ldo + col) = o;
+            }
+        }
+    }
 }
 
 template <int EPI>
@@ -244,13 +378,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
     const LoadPlan L = make_plan(p, m0, n0);
 #pragma unroll
-    for (int i = 0; i < NSTAGE; ++i)
-        if (i < S) issue_stage(p, L, lds + i * STAGE_BYTES, i);
-    // Stage 0 landed: at most min(S, 4) - 1 later stages still outstanding.
-    if (S >= 4) wait_vmcnt<3 * LOADS_PER_STAGE>();
-    else if (S == 3) wait_vmcnt<2 * LOADS_PER_STAGE>();
-    else if (S == 2) wait_vmcnt<LOADS_PER_STAGE>();
-    else wait_vmcnt<0>();
+    for (int i = 0; i < NSTAGE; ++i) issue_stage(p, L, lds + i * STAGE_BYTES, i < S ? i : S - 1);
+    wait_vmcnt<3 * LOADS_PER_STAGE>();  // stage 0 landed
     block_barrier();
     Frags fa, fb;
     read_frags(lds, wm, wn, lr, kh, fa);
@@ -260,65 +389,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         pipeline_step<0>(p, L, lds, s, S, acc, fa, fb, wm, wn, lr, kh);
         pipeline_step<1>(p, L, lds, s + 1, S, acc, fb, fa, wm, wn, lr, kh);
     }
+    wait_vmcnt<0>();  // the clamped tail loads must land before LDS is reused
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    block_barrier();
 
-    // ------------------------------------------------------------ epilogue
-    // Accumulator i of tile (ti, tj): row 8(i/4) + 4(l/32) + i%4, column l%32.
-    const int64_t wrow0 = m0 + wm * 128, wcol0 = n0 + wn * 128;
-    if constexpr (EPI == QIM_EPI_NONE || EPI == QIM_EPI_BIAS || EPI == QIM_EPI_GATED_RESIDUAL) {
-        uint16_t *out = reinterpret_cast<uint16_t *>(p.out);
-#pragma unroll
-        for (int tj = 0; tj < 4; ++tj) {
-            const int64_t col = wcol0 + tj * 32 + lr;
-            float bias = 0.0f;
-            if constexpr (EPI == QIM_EPI_BIAS) bias = bf16_to_f32(p.bias[col]);
-#pragma unroll
-            for (int ti = 0; ti < 4; ++ti) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int64_t row = wrow0 + ti * 32 + 8 * (i >> 2) + 4 * kh + (i & 3);
-                    if (row >= p.M) continue;
-                    float v = acc[ti][tj][i];
-                    if constexpr (EPI == QIM_EPI_BIAS) v = v + bias;
-                    if constexpr (EPI == QIM_EPI_GATED_RESIDUAL) {
-                        const float g = bf16_to_f32(p.gate[(row / p.seq) * p.N + col]);
-                        const float h = bf16_to_f32(p.res[row * p.N + col]);
-                        v = h + rbf(g * rbf(v));
-                    }
-                    out[row * p.ldo + col] = (uint16_t)(pack_bf16x2(v, 0.0f) & 0xffffu);
-                }
-            }
-        }
-    } else {
-        // SwiGLU: tiles tj = 2u (gate) and 2u + 1 (up) hold the same output
-        // columns (weight rows interleaved in groups of 32).
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int64_t ocol = wcol0 / 2 + u * 32 + lr;
-            const int64_t F = p.N / 2;
-#pragma unroll
-            for (int ti = 0; ti < 4; ++ti) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int64_t row = wrow0 + ti * 32 + 8 * (i >> 2) + 4 * kh + (i & 3);
-                    const float y = swiglu1(rbf(acc[ti][2 * u][i]), rbf(acc[ti][2 * u + 1][i]));
-                    if constexpr (EPI == QIM_EPI_SWIGLU) {
-                        if (row < p.M)
-                            reinterpret_cast<uint16_t *>(p.out)[row * p.ldo + ocol] =
-                                (uint16_t)(pack_bf16x2(y, 0.0f) & 0xffffu);
-                    } else {
-                        // One 32-element MX block = the 32 lanes of one half-wave.
-                        const uint32_t m = group_umax<32>(__float_as_uint(y) & 0x7fffffffu);
-                        const int e = mx_exponent(__uint_as_float(m));
-                        const uint8_t code = (uint8_t)(cvt_e4m3x4(y * mx_inverse(e), 0.f, 0.f, 0.f) & 0xffu);
-                        if (row < p.Mp) {
-                            reinterpret_cast<uint8_t *>(p.out)[row * F + ocol] = code;
-                            if (lr == 0) p.out_scales[mx_scale_offset(row, ocol >> 5, F)] = (uint8_t)e;
-                        }
-                    }
-                }
-            }
-        }
-    }
+    epilogue<EPI>(p, acc, lds, wm, wn, m0, n0, lane);
 }
 
 template <int EPI>
@@ -350,8 +425,11 @@ extern "C" int qim_mxfp8_gemm(const void *aq, const void *as, const void *bq, co
     const int64_t Mp = (M + 127) / 128 * 128;
     const int64_t tiles_m = (Mp + BM - 1) / BM, tiles_n = N / BN;
     QIM_REQUIRE(tiles_m * tiles_n < (1ll << 31), QIM_ERR_SHAPE, "qim_mxfp8_gemm: too many tiles");
-    QIM_REQUIRE(aligned16(aq) && aligned16(bq) && aligned16(as) && aligned16(bs), QIM_ERR_LAYOUT,
-                "qim_mxfp8_gemm: operands must be 16-byte aligned");
+    QIM_REQUIRE(aligned16(aq) && aligned16(bq) && aligned16(as) && aligned16(bs) && aligned16(out) &&
+                    (!res || aligned16(res)) && (!gate || aligned16(gate)) && (!out_scales || aligned16(out_scales)),
+                QIM_ERR_LAYOUT, "qim_mxfp8_gemm: operands must be 16-byte aligned");
+    QIM_REQUIRE(epilogue == QIM_EPI_SWIGLU_QUANT || ldo % 8 == 0, QIM_ERR_LAYOUT,
+                "qim_mxfp8_gemm: ldo=%lld is not a multiple of 8", (long long)ldo);
     QIM_REQUIRE(Mp * K < (1ll << 31) && N * K < (1ll << 31), QIM_ERR_SHAPE,
                 "qim_mxfp8_gemm: operands above 2 GiB are not supported");
     GemmArgs a{(const uint8_t *)aq, (const uint8_t *)as, (const uint8_t *)bq, (const uint8_t *)bs, M, Mp, N, K,

@@ -77,7 +77,7 @@ def lib():
                 if not os.path.exists(LIB_PATH):
                     raise NativeUnavailable(
                         f"{LIB_PATH} is not built; run qwen-image-2.1-accel_amd/build_native.py")
-                handle = ctypes.CDLL(LIB_PATH, mode=ctypes.RTLD_GLOBAL)
+                handle = ctypes.CDLL(LIB_PATH, mode=ctypes.RTLD_LOCAL)
                 for name, (res, args) in SIGNATURES.items():
                     fn = getattr(handle, name)
                     fn.restype = res
