@@ -259,17 +259,22 @@ def bench_block(tokens, steps, warmup):
 
 
 def bench_copy(steps, warmup):
-    """A plain device copy of 256 MiB: the achievable-bandwidth reference and
-    the calibration kernel of the FETCH_SIZE / WRITE_SIZE counters."""
+    """A streaming device copy of 256 MiB (qim_debug_copy: one 16-byte
+    non-temporal load and store per lane): the achievable-bandwidth reference
+    and the calibration kernel of the FETCH_SIZE / WRITE_SIZE counters."""
+    from qwen_image_accel import _native
     n = 256 << 20
     n_copies = copies_for(n)
     src = [torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1) for _ in range(n_copies)]
     dst = [torch.empty(n, dtype=torch.uint8, device="cuda") for _ in range(n_copies)]
+    L = _native.lib()
 
     def step(i):
-        dst[i % n_copies].copy_(src[i % n_copies])
+        j = i % n_copies
+        rc = L.qim_debug_copy(src[j].data_ptr(), dst[j].data_ptr(), n, torch.cuda.current_stream().cuda_stream)
+        assert rc == 0
     us = Timed(step, max(10, steps // 10), warmup).run() * 1e3
-    return dict(kernel="copy", us=us, bytes=2 * n, gbs=2 * n / us / 1e3, frac=2 * n / us / 1e3 / HBM_PEAK_GBS,
+    return dict(kernel="k_debug_copy", us=us, bytes=2 * n, gbs=2 * n / us / 1e3, frac=2 * n / us / 1e3 / HBM_PEAK_GBS,
                 shape="256 MiB")
 
 

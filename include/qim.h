@@ -152,6 +152,13 @@ int qim_debug_mfma_tile(const void *a, const void *b, const void *sa, const void
 /* Scale-routing probe of the scaled MFMA (shape 0: 32x32x64, 1: 16x16x128):
  * 4096 one-hot experiments, out: 4096 x 1024 (shape 0) or 4096 x 256 fp32. */
 int qim_debug_mfma_probe(int shape, float *out, void *stream);
+/* bf16(silu(g)) of n bf16 values with the rounding every SwiGLU kernel uses
+ * (reference kernels/bf16.py:17-22: bf16(g / (1 + exp(-g)))). */
+int qim_debug_silu(const void *g, void *out, int64_t n, void *stream);
+/* Streaming device copy of nbytes (a multiple of 16, 16-byte aligned): the
+ * bandwidth reference of the benchmarks and the calibration kernel of the HBM
+ * byte counters.  No reference counterpart. */
+int qim_debug_copy(const void *src, void *dst, int64_t nbytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -19,8 +19,8 @@ __global__ __launch_bounds__(256) void k_gated_residual(const uint16_t *__restri
     const uint32_t v = blockIdx.x * 256u + threadIdx.x;
     if (v >= nvec) return;
     const uint32_t b = v / batch_vec, c = v % d8;
-    const uint4 hv = reinterpret_cast<const uint4 *>(h)[v];
-    const uint4 xv = reinterpret_cast<const uint4 *>(x)[v];
+    const uint4 hv = ld_nt(reinterpret_cast<const uint4 *>(h) + v);
+    const uint4 xv = ld_nt(reinterpret_cast<const uint4 *>(x) + v);
     const uint4 gv = reinterpret_cast<const uint4 *>(gate)[b * d8 + c];
     float hf[8], xf[8], gf[8], o[8];
     unpack8(hv, hf);
@@ -28,7 +28,7 @@ __global__ __launch_bounds__(256) void k_gated_residual(const uint16_t *__restri
     unpack8(gv, gf);
 #pragma unroll
     for (int i = 0; i < 8; ++i) o[i] = hf[i] + rbf(gf[i] * xf[i]);
-    reinterpret_cast<uint4 *>(out)[v] = pack8(o);
+    st_nt(reinterpret_cast<uint4 *>(out) + v, pack8(o));
 }
 
 // swiglu(g, v) over strided rows (reference kernels/bf16.py:12-24).
@@ -38,14 +38,14 @@ __global__ __launch_bounds__(256) void k_swiglu(const uint16_t *__restrict__ g, 
     const uint32_t c = blockIdx.x * 256u + threadIdx.x;
     if (c >= f8) return;
     const int64_t row = blockIdx.y;
-    const uint4 gv = *reinterpret_cast<const uint4 *>(g + row * ldg + c * 8);
-    const uint4 vv = *reinterpret_cast<const uint4 *>(v + row * ldv + c * 8);
+    const uint4 gv = ld_nt(g + row * ldg + c * 8);
+    const uint4 vv = ld_nt(v + row * ldv + c * 8);
     float gf[8], vf[8], o[8];
     unpack8(gv, gf);
     unpack8(vv, vf);
 #pragma unroll
     for (int i = 0; i < 8; ++i) o[i] = silu_bf16(gf[i]) * vf[i];
-    *reinterpret_cast<uint4 *>(out + row * ldo + c * 8) = pack8(o);
+    st_nt(out + row * ldo + c * 8, pack8(o));
 }
 
 }  // namespace qim

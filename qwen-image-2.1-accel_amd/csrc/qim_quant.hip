@@ -19,7 +19,7 @@ struct QuantSource {
     const uint16_t *x;
     int64_t ldx;
     __device__ __forceinline__ void load(bool live, int64_t row, int64_t col, uint4 &a, uint4 &b) const {
-        a = live ? *reinterpret_cast<const uint4 *>(x + row * ldx + col) : make_uint4(0, 0, 0, 0);
+        a = live ? ld_nt(x + row * ldx + col) : make_uint4(0, 0, 0, 0);
         (void)b;
     }
     __device__ __forceinline__ void values(const uint4 &a, const uint4 &b, float *f) const {
@@ -37,8 +37,8 @@ struct SwigluSource {
     const uint16_t *v;
     int64_t ldv;
     __device__ __forceinline__ void load(bool live, int64_t row, int64_t col, uint4 &a, uint4 &b) const {
-        a = live ? *reinterpret_cast<const uint4 *>(g + row * ldg + col) : make_uint4(0, 0, 0, 0);
-        b = live ? *reinterpret_cast<const uint4 *>(v + row * ldv + col) : make_uint4(0, 0, 0, 0);
+        a = live ? ld_nt(g + row * ldg + col) : make_uint4(0, 0, 0, 0);
+        b = live ? ld_nt(v + row * ldv + col) : make_uint4(0, 0, 0, 0);
     }
     __device__ __forceinline__ void values(const uint4 &a, const uint4 &b, float *f) const {
         float gg[8], vv[8];
@@ -87,7 +87,7 @@ __global__ __launch_bounds__(256) void k_quant_tile(Source src, uint8_t *__restr
         src.values(a[i], b[i], f);
         int e;
         uint2 c = quantize8(f, e);
-        *reinterpret_cast<uint2 *>(q + (row0 + r) * K + col) = c;
+        st_nt(q + (row0 + r) * K + col, c);
         if ((c16 & 3) == 0) sb[(r & 31) * 16 + wave * 4 + (c16 >> 2)] = (uint8_t)e;
     }
     __syncthreads();

@@ -111,9 +111,43 @@ __global__ void k_debug_mfma_probe(float *__restrict__ out) {
     }
 }
 
+__global__ void k_debug_silu(const uint16_t *__restrict__ g, uint16_t *__restrict__ out, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = (uint16_t)(__float_as_uint(silu_bf16(bf16_to_f32(g[i]))) >> 16);
+}
+
+// Streaming copy, one 16-byte vector per lane: the achievable-bandwidth
+// reference and the calibration kernel of the HBM byte counters.
+__global__ __launch_bounds__(256) void k_debug_copy(const uint4 *__restrict__ src, uint4 *__restrict__ dst,
+                                                     int64_t nvec) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < nvec) st_nt(dst + i, ld_nt(src + i));
+}
+
 }  // namespace qim
 
 using namespace qim;
+
+extern "C" int qim_debug_silu(const void *g, void *out, int64_t n, void *stream) {
+    QIM_REQUIRE(g && out && n >= 0, QIM_ERR_ARG, "qim_debug_silu: bad arguments");
+    QIM_REQUIRE((n + 255) / 256 < (1ll << 31), QIM_ERR_SHAPE, "qim_debug_silu: too large");
+    if (n == 0) return QIM_OK;
+    hipLaunchKernelGGL(k_debug_silu, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, as_stream(stream),
+                       (const uint16_t *)g, (uint16_t *)out, n);
+    return check_launch("qim_debug_silu");
+}
+
+extern "C" int qim_debug_copy(const void *src, void *dst, int64_t nbytes, void *stream) {
+    QIM_REQUIRE(src && dst && nbytes >= 0, QIM_ERR_ARG, "qim_debug_copy: bad arguments");
+    QIM_REQUIRE(nbytes % 16 == 0 && aligned16(src) && aligned16(dst), QIM_ERR_LAYOUT,
+                "qim_debug_copy: 16-byte aligned operands and size required");
+    const int64_t nvec = nbytes / 16;
+    QIM_REQUIRE((nvec + 255) / 256 < (1ll << 31), QIM_ERR_SHAPE, "qim_debug_copy: too large");
+    if (nvec == 0) return QIM_OK;
+    hipLaunchKernelGGL(k_debug_copy, dim3((unsigned)((nvec + 255) / 256)), dim3(256), 0, as_stream(stream),
+                       (const uint4 *)src, (uint4 *)dst, nvec);
+    return check_launch("qim_debug_copy");
+}
 
 extern "C" int qim_debug_mfma_probe(int shape, float *out, void *stream) {
     QIM_REQUIRE(out && (shape == 0 || shape == 1), QIM_ERR_ARG, "qim_debug_mfma_probe: bad arguments");

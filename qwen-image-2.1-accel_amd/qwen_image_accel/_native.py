@@ -58,6 +58,8 @@ SIGNATURES = {
     "qim_debug_bf16_round": (_C, [_P, _P, _I, _P]),
     "qim_debug_mfma_tile": (_C, [_P, _P, _P, _P, _P, _P]),
     "qim_debug_mfma_probe": (_C, [_C, _P, _P]),
+    "qim_debug_copy": (_C, [_P, _P, _I, _P]),
+    "qim_debug_silu": (_C, [_P, _P, _I, _P]),
 }
 
 _lib = None

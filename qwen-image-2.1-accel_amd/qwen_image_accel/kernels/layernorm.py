@@ -6,7 +6,7 @@ rounding of each op.  The keyword-only extras default to the reference's
 behaviour; with them the call computes the full modulated residual branch
 ``residual + gate * ((1 + scale) * LN(x) + shift)`` in one HBM pass, a bf16
 rounding after every eager op.  The kernel is libqim's ``qim_adaln`` (any
-D % 8 == 0 up to 8192; the reference kernel is fixed to D = 4096).
+D % 8 == 0 up to 16384; the reference kernel is fixed to D = 4096).
 
 Unsupported inputs (CPU tensors, other dtypes, non-contiguous x, an affine
 norm) take the eager composition, as the reference's guard does
@@ -42,7 +42,7 @@ def native_supported(x, scale, norm, shift=None, gate=None, residual=None):
             or x.numel() == 0):
         return False
     d = x.shape[-1]
-    if d % 8 or d > 8192:
+    if d % 8 or d > 16384:
         return False
     if not (_vec_ok(scale, x) and _vec_ok(shift, x) and _vec_ok(gate, x)):
         return False

@@ -90,6 +90,37 @@ def test_scaled_mfma_lane_layout(dev):
     assert rel_fro(got, ref) < 1e-3
 
 
+def test_silu_exhaustive(dev):
+    """The fast SiLU (estimate + rounding-band check + exact fallback) equals
+    the oracle's bf16(g / (1 + expf(-g))) on every one of the 65536 bf16
+    inputs, so every SwiGLU kernel's silu is pinned for all inputs."""
+    raw = np.arange(65536, dtype=np.uint16)
+    g = bf16_values(raw)
+    say("silu exhaustive")
+    x = torch.from_numpy(raw.view(np.int16)).to(dev)
+    out = torch.empty(65536, dtype=torch.int16, device=dev)
+    _native.call("qim_debug_silu", _native.ptr(x), _native.ptr(out), 65536, _native.stream())
+    got = out.cpu().numpy().view(np.uint16)
+    # swiglu(g, 1) = bf16(bf16(silu(g)) * 1) = bf16(silu(g)).
+    ref = O.swiglu(raw.reshape(1, -1), O.f32_to_bf16(np.ones((1, 65536), np.float32))).reshape(-1)
+    nan = np.isnan(g)
+    assert np.array_equal(np.isnan(bf16_values(got))[~nan], np.isnan(bf16_values(ref))[~nan])
+    bad = np.where((got != ref) & ~nan)[0]
+    assert bad.size == 0, [(hex(raw[i]), hex(got[i]), hex(ref[i])) for i in bad[:10]]
+    assert np.all(np.isnan(bf16_values(got)[nan]))
+
+
+def test_streaming_copy(dev):
+    """The bandwidth/counter calibration copy moves every byte, tail included."""
+    n = (3 << 20) + 48
+    say("copy", n)
+    src = torch.randint(0, 256, (n,), dtype=torch.uint8).to(dev)
+    dst = torch.zeros(n + 16, dtype=torch.uint8, device=dev)
+    _native.call("qim_debug_copy", _native.ptr(src), _native.ptr(dst), n, _native.stream())
+    got = dst.cpu()
+    assert torch.equal(got[:n], src.cpu()) and int(got[n:].sum()) == 0
+
+
 # ---------------------------------------------------------------- quantize --
 
 @pytest.mark.parametrize("m,k", [(128, 4096), (1024, 4096), (1536, 4096), (2400, 4096), (4096, 12288),
@@ -163,6 +194,36 @@ def test_adaln_config1_full_chain(dev):
     ref = O.adaln(bits(x), bits(scale), bits(shift), bits(gate), bits(res), add_one=True)
     ok, worst = bf16_close_chain(bits(out), ref)
     assert ok, worst
+
+
+@pytest.mark.parametrize("d", [136, 1000, 3072, 16384])
+@pytest.mark.parametrize("parts", ["shift", "gate+res", "shift+res", "all-no-add-one"])
+def test_adaln_optional_operands_and_widths(dev, d, parts):
+    """Every subset of the optional operands (an absent one is a neutral value
+    in the kernel, so signed zeros must survive) at widths that leave part of
+    the last wave idle (136, 1000) and at the largest supported width."""
+    g = torch.Generator().manual_seed(d)
+    x = bf16_randn(g, (2, 37, d))
+    x[0, 3] = 0.0                                      # a constant row: t0 = 0 (signed zeros)
+    scale = bf16_randn(g, (2, 1, d), 0.1)
+    scale[..., ::7] = -1.0                             # 1 + scale = 0 -> t2 = +-0
+    scale[..., 1::7] = -3.0                            # 1 + scale < 0 -> t2 = -0 on the zero row
+    shift = bf16_randn(g, (2, 1, d), 0.1) if "shift" in parts or "all" in parts else None
+    gate = bf16_randn(g, (2, 1, d), 0.1) if "gate" in parts or "all" in parts else None
+    res = bf16_randn(g, (2, 37, d)) if "res" in parts or "all" in parts else None
+    add_one = "no-add-one" not in parts
+    say("adaln parts", d, parts)
+    dv = (lambda t: None if t is None else t.to(dev))
+    out = layernorm.layer_norm_scale(x.to(dev), scale.to(dev), _LN(d), shift=dv(shift), gate=dv(gate),
+                                     residual=dv(res), add_one=add_one)
+    assert _native.calls.get("qim_adaln", 0) > 0
+    nb = (lambda t: None if t is None else bits(t))
+    ref = O.adaln(bits(x), bits(scale), nb(shift), nb(gate), nb(res), add_one=add_one)
+    ok, worst = bf16_close_chain(bits(out), ref)
+    assert ok, worst
+    # Rows whose LayerNorm output is exactly zero carry the reference's signed zeros.
+    zrow = bits(out)[0, 3]
+    assert np.array_equal(zrow, ref[0, 3])
 
 
 @pytest.mark.parametrize("b,n,d", [(1, 1024, 4096), (1, 77, 4096), (2, 1024, 4096), (1, 4352, 3072),

@@ -49,7 +49,7 @@ def test_abi_version():
     ("qim_gated_residual", (16, 16, 16, 16, 4, 12, 4, None), _native.QIM_ERR_SHAPE),
     ("qim_swiglu", (16, 8, 16, 8, 16, 4, 1, 8, None), _native.QIM_ERR_LAYOUT),
     ("qim_rms_norm", (16, 16, 16, 4, 96, 1e-6, None), _native.QIM_ERR_SHAPE),
-    ("qim_adaln", (16, 16, None, None, None, 16, 1, 8200, 1, 1e-6, 0, None), _native.QIM_ERR_SHAPE),
+    ("qim_adaln", (16, 16, None, None, None, 16, 1, 16392, 1, 1e-6, 0, None), _native.QIM_ERR_SHAPE),
     ("qim_adaln_quantize", (16, 16, None, None, None, 16, 16, 1, 3000, 1, 1e-6, 0, None),
      _native.QIM_ERR_SHAPE),
     ("qim_mxfp8_gemm", (16, 16, 16, 16, 4, 384, 128, 0, None, None, None, 0, 16, 384, None, None),
