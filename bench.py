@@ -278,6 +278,17 @@ def bench_copy(steps, warmup):
                 shape="256 MiB")
 
 
+def measured_traffic(entry):
+    """HBM bytes per launch of `entry`'s kernel, from the committed rocprofv3
+    counter runs (FETCH_SIZE and WRITE_SIZE, calibrated on a copy of known
+    size); None when no measurement is recorded."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "traffic.json")) as fh:
+            return json.load(fh)["kernels"][entry]["traffic_bytes"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 # ------------------------------------------------------------ CPU baseline --
 
 def cpu_baseline(seconds):
@@ -365,8 +376,10 @@ def main():
     }
     if head:
         out["roofline"] = {"bound": "hbm", "achieved": round(head["gbs"], 1), "peak": HBM_PEAK_GBS,
-                           "unit": "GB/s", "frac": round(head["frac"], 4), "traffic": None,
-                           "kernel": head["kernel"], "algorithmic_bytes": head["bytes"]}
+                           "unit": "GB/s", "frac": round(head["frac"], 4), "traffic": measured_traffic(head["kernel"]),
+                           "kernel": head["kernel"], "algorithmic_bytes": head["bytes"],
+                           "traffic_source": "profiles/traffic.json: rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE per "
+                                             "dispatch, each scaled by its reading for a 256 MiB copy"}
     summary = {}
     for k, v in comp.items():
         e = {"us": round(v["us"], 2)}
