@@ -161,6 +161,53 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// fp64 versions of the lane moves (each half moved separately) and of
+// group_sum, for the row statistics of the normalisations.
+template <int CTRL>
+__device__ __forceinline__ double dpp_mov(double v) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint64_t lo = dpp_mov<CTRL>((uint32_t)u), hi = dpp_mov<CTRL>((uint32_t)(u >> 32));
+    return __builtin_bit_cast(double, lo | (hi << 32));
+}
+template <int MASK>
+__device__ __forceinline__ double xor_lane(double v) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint64_t lo = xor_lane<MASK>((uint32_t)u), hi = xor_lane<MASK>((uint32_t)(u >> 32));
+    return __builtin_bit_cast(double, lo | (hi << 32));
+}
+template <int WIDTH>
+__device__ __forceinline__ double group_sum(double v) {
+    if constexpr (WIDTH >= 2) v += dpp_mov<DPP_QUAD_XOR1>(v);
+    if constexpr (WIDTH >= 4) v += dpp_mov<DPP_QUAD_XOR2>(v);
+    if constexpr (WIDTH >= 8) v += dpp_mov<DPP_HALF_MIRROR>(v);
+    if constexpr (WIDTH >= 16) v += dpp_mov<DPP_ROW_MIRROR>(v);
+    if constexpr (WIDTH >= 32) v += xor_lane<16>(v);
+    if constexpr (WIDTH >= 64) v += xor_lane<32>(v);
+    return v;
+}
+
+// Reciprocal square root of (var + eps) as the normalisations' reference
+// statistics define it: t = var + eps in fp32, then R = fp32(1 / sqrt(t))
+// evaluated in float64 (IEEE sqrt and divide) and rounded once.
+//
+// Fast path with the same result: y = v_rsq_f32(t) (relative error < 2^-22)
+// refined by two float64 Newton steps (error < 2^-50 after the second), so
+// the exact 1/sqrt(t) and the float64 value of R both lie within
+// y (1 +- 2^-40).  When both ends of that interval round to the same fp32
+// value, so does everything inside it, R included; otherwise (a value within
+// 2^-40 of an fp32 rounding midpoint, or a non-finite or non-positive t,
+// where the Newton steps give NaN) the float64 expression is evaluated.
+__device__ __forceinline__ float rstd_of(float var, float eps) {
+    const float t = var + eps;
+    const double td = (double)t;
+    double y = (double)__builtin_amdgcn_rsqf(t);
+    y = __builtin_fma(y, __builtin_fma(-td * y, y, 1.0) * 0.5, y);
+    y = __builtin_fma(y, __builtin_fma(-td * y, y, 1.0) * 0.5, y);
+    const float lo = (float)(y * (1.0 - 0x1p-40)), hi = (float)(y * (1.0 + 0x1p-40));
+    if (__builtin_expect(lo == hi, 1)) return lo;
+    return (float)(1.0 / sqrt(td));
+}
+
 template <int WIDTH>
 __device__ __forceinline__ uint32_t group_umax(uint32_t v) {
     uint32_t o;

@@ -2,12 +2,13 @@
 // gate and residual, its MXFP8-producing variant, per-head RMSNorm, complex
 // RoPE, and the fused QK-RMSNorm + RoPE + prefix K/V pack.
 //
-// LayerNorm: one wave per row; lane l holds the 16-byte vectors l, l+64, ...
-// of the row in registers (D = 3072 -> 6 vectors), so the row is read from HBM
-// exactly once; mean and variance are exact two-pass fp32 sums reduced across
-// the wave.  RMSNorm/RoPE: one head row of D = 128 is 16 lanes x 8 bf16; the
-// sum of squares is reduced inside the 16-lane group and the RoPE pairs
-// (x[2j], x[2j+1]) sit in the same lane, so no data leaves the lane.
+// LayerNorm: one workgroup per row; lane l of the W waves holds the 16-byte
+// vectors l, l + 64 W, ... of the row in registers, so the row is read from
+// HBM exactly once; mean and variance are two-pass float64 sums reduced across
+// the workgroup and rounded once to fp32.  RMSNorm/RoPE: one head row of
+// D = 128 is 16 lanes x 8 bf16; the float64 sum of squares is reduced inside
+// the 16-lane group and the RoPE pairs (x[2j], x[2j+1]) sit in the same lane,
+// so no data leaves the lane.
 #include "qim_device.h"
 #include "qim_runtime.h"
 
@@ -27,36 +28,50 @@ struct AdaLNArgs {
     int flags;
 };
 
-constexpr int ADALN_NV = 2;            // 16-byte vectors per lane
-constexpr int ADALN_MAX_WAVES = 16;    // 1024 threads: D <= 16384
+constexpr int ADALN_MAX_WAVES = 16;    // 1024 threads per row (masked kernel)
+constexpr int ADALN_FULL_WAVES = 4;    // full-coverage kernels: 256 threads, no register cap below 512
 
 // bf16x2 words of the neutral operand of each optional step: adding -0 and
-// multiplying by 1 return a bf16 value unchanged (signed zeros included), so
-// an absent shift, gate or residual costs arithmetic but no branch.
+// multiplying by 1 return a bf16 value unchanged (signed zeros included).
 constexpr uint32_t BF16X2_NEG_ZERO = 0x80008000u, BF16X2_ONE = 0x3f803f80u;
 
 // One modulated LayerNorm row per workgroup of W waves (reference chain, eager
 // rounding points: t0 = bf16(LN x), t1 = scale or bf16(1 + scale),
 // t2 = bf16(t1 t0), t3 = bf16(t2 + shift), t4 = bf16(gate t3),
 // out = bf16(res + t4); kernels/layernorm.py:49-55, kernels/epilogue.py:127-133).
-// Thread t holds vectors t and t + 64 W of the row; the two-pass statistics
-// are reduced inside each wave, then across the W waves through LDS.  Every
-// load is issued before the first reduction.
-template <bool QUANT>
-__global__ __launch_bounds__(1024) void k_adaln(AdaLNArgs p) {
-    constexpr int NV = ADALN_NV;
-    __shared__ float red[2][ADALN_MAX_WAVES];
+// Thread t holds the 16-byte vectors t, t + 64 W, ... (NV of them) of the row;
+// the two-pass float64 statistics are reduced inside each wave, then across
+// the W waves through LDS.  Every load is issued before the first reduction.
+// FULL: the W * 64 * NV vectors cover the row exactly (D = 3072: NV 3, W 2),
+// so no lane tests its index and the optional operands are wave-uniform
+// branches; otherwise lanes past the row end hold zeros (any D % 8 == 0).
+// Two waves of three vectors per lane was the fastest split of config 1
+// measured on MI355X.
+template <bool QUANT, int NV, bool FULL>
+__global__ __launch_bounds__(FULL ? 64 * ADALN_FULL_WAVES : 64 * ADALN_MAX_WAVES) void k_adaln(AdaLNArgs p) {
+    __shared__ double red[2][FULL ? ADALN_FULL_WAVES : ADALN_MAX_WAVES];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nthr = blockDim.x, nw = nthr >> 6;
     const int64_t row = blockIdx.x;
     const int nvec = p.D >> 3;
-    const bool live = row < p.rows;
-    const int64_t b = live ? row / p.seq : 0;
+    if (row >= p.rows) {
+        // Padding row of the quantized output: codes 0, exponents 0.
+        if constexpr (QUANT) {
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+                const int j = tid + nthr * i;
+                if (!FULL && j >= nvec) break;
+                st_nt(reinterpret_cast<uint2 *>(p.q + row * p.D) + j, make_uint2(0, 0));
+                if ((lane & 15) == 0)
+                    *reinterpret_cast<uint32_t *>(p.qs + mx_scale_offset(row, j >> 2, p.D)) = 0u;
+            }
+        }
+        return;
+    }
+    const uint32_t b = (uint32_t)row / (uint32_t)p.seq;
     const uint4 *xr = reinterpret_cast<const uint4 *>(p.x + row * p.D);
-    const uint4 *rr = p.res ? reinterpret_cast<const uint4 *>(p.res + row * p.D) : nullptr;
-    const uint4 *sc = reinterpret_cast<const uint4 *>(p.scale + b * p.D);
-    const uint4 *sh = p.shift ? reinterpret_cast<const uint4 *>(p.shift + b * p.D) : nullptr;
-    const uint4 *ga = p.gate ? reinterpret_cast<const uint4 *>(p.gate + b * p.D) : nullptr;
+    const uint4 *sc = reinterpret_cast<const uint4 *>(p.scale + (int64_t)b * p.D);
+    const uint4 zero = make_uint4(0, 0, 0, 0);
     const uint4 neg0 = make_uint4(BF16X2_NEG_ZERO, BF16X2_NEG_ZERO, BF16X2_NEG_ZERO, BF16X2_NEG_ZERO);
     const uint4 one = make_uint4(BF16X2_ONE, BF16X2_ONE, BF16X2_ONE, BF16X2_ONE);
 
@@ -64,52 +79,86 @@ __global__ __launch_bounds__(1024) void k_adaln(AdaLNArgs p) {
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         const int j = tid + nthr * i;
-        const bool ok = live && j < nvec;
-        xv[i] = ok ? ld_nt(xr + j) : make_uint4(0, 0, 0, 0);
-        rv[i] = (ok && rr) ? ld_nt(rr + j) : neg0;
-        sv[i] = ok ? sc[j] : make_uint4(0, 0, 0, 0);
-        hv[i] = (ok && sh) ? sh[j] : neg0;
-        gv[i] = (ok && ga) ? ga[j] : one;
+        const bool ok = FULL || j < nvec;
+        xv[i] = ok ? ld_nt(xr + j) : zero;
+        sv[i] = ok ? sc[j] : zero;
+    }
+    if (p.res) {
+        const uint4 *rr = reinterpret_cast<const uint4 *>(p.res + row * p.D);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int j = tid + nthr * i;
+            rv[i] = (FULL || j < nvec) ? ld_nt(rr + j) : neg0;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) rv[i] = neg0;
+    }
+    if (p.shift) {
+        const uint4 *sh = reinterpret_cast<const uint4 *>(p.shift + (int64_t)b * p.D);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int j = tid + nthr * i;
+            hv[i] = (FULL || j < nvec) ? sh[j] : neg0;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) hv[i] = neg0;
+    }
+    if (p.gate) {
+        const uint4 *ga = reinterpret_cast<const uint4 *>(p.gate + (int64_t)b * p.D);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int j = tid + nthr * i;
+            gv[i] = (FULL || j < nvec) ? ga[j] : one;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) gv[i] = one;
     }
     float x[NV][8];
 #pragma unroll
     for (int i = 0; i < NV; ++i) unpack8(xv[i], x[i]);
 
-    // Two-pass statistics in fp32 (absent vectors hold zeros and add nothing).
-    float s = 0.0f;
+    // Row statistics in float64: the sum of the row's bf16 values is exact (it
+    // does not depend on the reduction order); the mean and the biased
+    // variance (two passes) are rounded once to fp32.  Absent vectors hold
+    // zeros and add nothing.
+    double s = 0.0;
 #pragma unroll
     for (int i = 0; i < NV; ++i)
 #pragma unroll
-        for (int t = 0; t < 8; ++t) s += x[i][t];
+        for (int t = 0; t < 8; ++t) s += (double)x[i][t];
     s = group_sum<64>(s);
     if (lane == 0) red[0][wave] = s;
     __syncthreads();
-    s = 0.0f;
+    s = 0.0;
     for (int w = 0; w < nw; ++w) s += red[0][w];
-    const float mean = s / (float)p.D;
-    float ss = 0.0f;
+    const double mean_d = s / (double)p.D;
+    double ss = 0.0;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-        const bool ok = tid + nthr * i < nvec;
+        const bool ok = FULL || tid + nthr * i < nvec;
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
-            const float d = ok ? x[i][t] - mean : 0.0f;
-            ss = __builtin_fmaf(d, d, ss);
+            const double d = ok ? (double)x[i][t] - mean_d : 0.0;
+            ss += d * d;
         }
     }
     ss = group_sum<64>(ss);
     if (lane == 0) red[1][wave] = ss;
     __syncthreads();
-    ss = 0.0f;
+    ss = 0.0;
     for (int w = 0; w < nw; ++w) ss += red[1][w];
-    const float rstd = 1.0f / sqrtf(ss / (float)p.D + p.eps);
+    const float mean = (float)mean_d;
+    const float rstd = rstd_of((float)(ss / (double)p.D), p.eps);
     // t1 = bf16(scale + 1) with add_one, else scale (+ -0 leaves it unchanged).
     const float scale_add = (p.flags & QIM_ADALN_ADD_ONE) ? 1.0f : -0.0f;
 
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         const int j = tid + nthr * i;
-        if (j >= nvec) break;  // uniform inside each 16-lane group when D % 128 == 0
+        if (!FULL && j >= nvec) break;  // uniform inside each 16-lane group when D % 128 == 0
         float sf[8], hf[8], gf[8], rf[8], o[8];
         unpack8(sv[i], sf);
         unpack8(hv[i], hf);
@@ -132,10 +181,6 @@ __global__ __launch_bounds__(1024) void k_adaln(AdaLNArgs p) {
             rbf2(a0, a1);                                             // t4
             o[t] = rf[t] + a0;
             o[t + 1] = rf[t + 1] + a1;
-        }
-        if (!live) {
-#pragma unroll
-            for (int t = 0; t < 8; ++t) o[t] = 0.0f;  // padding rows of the quantized output
         }
         if constexpr (!QUANT) {
             st_nt(reinterpret_cast<uint4 *>(p.out + row * p.D) + j, pack8(o));
@@ -165,13 +210,36 @@ __global__ __launch_bounds__(1024) void k_adaln(AdaLNArgs p) {
     }
 }
 
+// Picks the split of a row: full coverage with NV in {3, 4, 2, 1} vectors per
+// lane (the first that divides D/8 into at most 4 whole waves; D = 3072: 3 x 2,
+// D = 4096: 4 x 2), else the masked kernel with 2 vectors per lane.
 template <bool QUANT>
 static int launch_adaln(const AdaLNArgs &a, hipStream_t st) {
     const int nvec = a.D / 8;
-    const int waves = (nvec + 64 * ADALN_NV - 1) / (64 * ADALN_NV);
-    if (waves > ADALN_MAX_WAVES) return fail(QIM_ERR_SHAPE, "adaln: D=%d exceeds %d", a.D, 8 * 64 * ADALN_NV * ADALN_MAX_WAVES);
-    if (a.rows_pad >= (1ll << 31)) return fail(QIM_ERR_SHAPE, "adaln: too many rows");
-    hipLaunchKernelGGL((k_adaln<QUANT>), dim3((unsigned)a.rows_pad), dim3(64 * waves), 0, st, a);
+    if (a.rows_pad >= (1ll << 31) || a.seq >= (1ll << 31)) return fail(QIM_ERR_SHAPE, "adaln: too many rows");
+    const dim3 grid((unsigned)a.rows_pad);
+    if (nvec % 64 == 0) {
+        const int k = nvec / 64;
+        if (k % 3 == 0 && k / 3 <= ADALN_FULL_WAVES) {
+            hipLaunchKernelGGL((k_adaln<QUANT, 3, true>), grid, dim3(64 * (k / 3)), 0, st, a);
+            return QIM_OK;
+        }
+        if (k % 4 == 0 && k / 4 <= ADALN_FULL_WAVES) {
+            hipLaunchKernelGGL((k_adaln<QUANT, 4, true>), grid, dim3(64 * (k / 4)), 0, st, a);
+            return QIM_OK;
+        }
+        if (k % 2 == 0 && k / 2 <= ADALN_FULL_WAVES) {
+            hipLaunchKernelGGL((k_adaln<QUANT, 2, true>), grid, dim3(64 * (k / 2)), 0, st, a);
+            return QIM_OK;
+        }
+        if (k <= ADALN_FULL_WAVES) {
+            hipLaunchKernelGGL((k_adaln<QUANT, 1, true>), grid, dim3(64 * k), 0, st, a);
+            return QIM_OK;
+        }
+    }
+    const int waves = (nvec + 127) / 128;
+    if (waves > ADALN_MAX_WAVES) return fail(QIM_ERR_SHAPE, "adaln: D=%d exceeds %d", a.D, 8 * 128 * ADALN_MAX_WAVES);
+    hipLaunchKernelGGL((k_adaln<QUANT, 2, false>), grid, dim3(64 * waves), 0, st, a);
     return QIM_OK;
 }
 
@@ -181,12 +249,24 @@ struct NormRopeArgs {
     const uint16_t *q, *k, *v, *ck, *cv, *wq, *wk;
     const float *freqs;  // (S, D/2) complex64 = (S, D) fp32 (cos, sin interleaved)
     uint16_t *oq, *ok, *ov;
-    int64_t rows;        // B * S * H
+    int64_t T;           // tokens B * S
     int64_t S, P, H;
     int64_t ldt;         // elements between consecutive tokens of q, k, v (>= H * D)
     float epsq, epsk;
+    uint32_t groups;     // head groups of one tensor of one token
+    uint32_t main_waves; // waves of the norm/rope part: T * tensors * groups
     int64_t main_blocks; // workgroups of the norm/rope part; the rest copy the prefix
 };
+
+// Head rows per lane of one wave: a wave owns U * (64 / (D / 8)) heads of one
+// tensor of one token (12 at D = 128 with U = 3).  Three 16-byte loads per
+// lane in flight was the fastest split of config 2 measured on MI355X (one
+// wave per token with all of its Q and K heads was 27% slower: every wave then
+// loads for the whole kernel's duration before its first store).  The launch
+// picks U in {3, 4, 2} so that the heads divide into whole waves (H = 24: 3;
+// H = 32: 4) and no lane tests its head index; other head counts take the
+// masked kernel with U = 3.
+constexpr int NR_ROWS = 3;
 
 // Normalise (optionally) and rotate (optionally) one 8-value chunk of a head
 // row; LPR lanes share the row.  Roundings are paired (one v_cvt_pk_bf16_f32
@@ -197,11 +277,13 @@ __device__ __forceinline__ uint4 norm_rope_chunk(const uint4 &xv, const float *w
     float x[8];
     unpack8(xv, x);
     if constexpr (NORM) {
-        float ss = 0.0f;
+        // Sum of squares in float64: exact for bf16 inputs, so independent of
+        // the reduction order; rounded once to the fp32 mean.
+        double ss = 0.0;
 #pragma unroll
-        for (int t = 0; t < 8; ++t) ss = __builtin_fmaf(x[t], x[t], ss);
+        for (int t = 0; t < 8; ++t) ss += (double)x[t] * (double)x[t];
         ss = group_sum<LPR>(ss);
-        const float r = 1.0f / sqrtf(ss / (float)(LPR * 8) + eps);
+        const float r = rstd_of((float)(ss / (double)(LPR * 8)), eps);
 #pragma unroll
         for (int t = 0; t < 8; t += 2) {
             float a = x[t] * r, b = x[t + 1] * r;
@@ -232,71 +314,73 @@ __device__ __forceinline__ uint4 norm_rope_chunk(const uint4 &xv, const float *w
 }
 
 // q/k: (B, S, H, D) -> oq (B, S, H, D), ok (B, P+S, H, D); v -> ov at the
-// packed index; the last (gridDim.x - main_blocks) workgroups copy the
-// cached prefix ck/cv (B, P, H, D) in front of each batch's rows.
+// packed index; the last (gridDim.x - main_blocks) workgroups copy the cached
+// prefix ck/cv (B, P, H, D) in front of each batch's rows.
 //
-// One wave per token: its LPR-lane groups walk the token's heads (RPI heads per
-// instruction), so each lane loads its 8-value slice of the RoPE table and of
-// the two norm weights once and reuses them for every head; all loads of the
-// token are issued before any arithmetic.  Head slots past H are skipped (for
-// H % RPI == 0 a whole wave skips them together).
-template <int D, bool NORM, bool ROPE, bool HAS_K, bool HAS_V>
+// Wave w of the main part owns head group w % groups of tensor
+// (w / groups) % NTENS (0 = q, 1 = k, 2 = v) of token w / (NTENS * groups):
+// NR_ROWS head rows per lane, LPR lanes per row, all loads issued before any
+// arithmetic.  Neighbouring waves share a token, so its RoPE row is read from
+// HBM once and from L2 by the others.  Head slots past H are skipped (uniform
+// over the LPR lanes of a row).  v is copied unchanged.
+template <int D, bool NORM, bool ROPE, int NTENS, int U, bool FULL>
 __global__ __launch_bounds__(256) void k_norm_rope(NormRopeArgs p) {
     constexpr int LPR = D / 8;       // lanes per head row
     constexpr int RPI = 64 / LPR;    // head rows per wave instruction
-    constexpr int UNROLL = 8;        // head rows in flight per lane
     const int lane = threadIdx.x & 63;
     const int g = lane / LPR, c = lane % LPR;
     if ((int64_t)blockIdx.x < p.main_blocks) {
-        const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // token, 0 .. B*S-1
-        if (t * p.H >= p.rows) return;                                   // whole wave
-        const int64_t bb = t / p.S, tok = t - bb * p.S;
+        const uint32_t w = blockIdx.x * 4u + (threadIdx.x >> 6);
+        if (w >= p.main_waves) return;  // whole wave
+        const uint32_t per_token = NTENS * p.groups;
+        const uint32_t t = w / per_token;
+        const uint32_t r = w - t * per_token;
+        const uint32_t tensor = r / p.groups;  // wave-uniform
+        const int h0 = (int)(r - tensor * p.groups) * (RPI * U) + g;
         const int H = (int)p.H;
+        const uint32_t bb = t / (uint32_t)p.S, tok = t - bb * (uint32_t)p.S;
+        const uint16_t *src = (tensor == 0 ? p.q : tensor == 1 ? p.k : p.v) + (int64_t)t * p.ldt + c * 8;
+        uint16_t *dst;
+        if (tensor == 0) {
+            dst = p.oq + (int64_t)t * H * D + c * 8;
+        } else {
+            const int64_t kv_row = ((int64_t)bb * (p.P + p.S) + p.P + tok) * H;
+            dst = (tensor == 1 ? p.ok : p.ov) + kv_row * D + c * 8;
+        }
+        uint4 x[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int h = h0 + u * RPI;
+            if (FULL || h < H) x[u] = ld_nt(src + (int64_t)h * D);
+        }
+        if (NTENS == 3 && tensor == 2) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int h = h0 + u * RPI;
+                if (FULL || h < H) st_nt(dst + (int64_t)h * D, x[u]);
+            }
+            return;
+        }
         float4 f0 = make_float4(0.f, 0.f, 0.f, 0.f), f1 = f0;
         if constexpr (ROPE) {
-            const float4 *fr = reinterpret_cast<const float4 *>(p.freqs + tok * D + c * 8);
+            const float4 *fr = reinterpret_cast<const float4 *>(p.freqs + (int64_t)tok * D + c * 8);
             f0 = fr[0];
             f1 = fr[1];
         }
-        float wq[8], wk[8];
-        if constexpr (NORM) {
-            unpack8(*reinterpret_cast<const uint4 *>(p.wq + c * 8), wq);
-            if constexpr (HAS_K) unpack8(*reinterpret_cast<const uint4 *>(p.wk + c * 8), wk);
-        }
-        const uint16_t *qsrc = p.q + t * p.ldt + c * 8;
-        const uint16_t *ksrc = HAS_K ? p.k + t * p.ldt + c * 8 : nullptr;
-        const uint16_t *vsrc = HAS_V ? p.v + t * p.ldt + c * 8 : nullptr;
-        uint16_t *qdst = p.oq + t * H * D + c * 8;
-        const int64_t kv_row = (bb * (p.P + p.S) + p.P + tok) * H;
-        for (int h0 = 0; h0 < H; h0 += RPI * UNROLL) {
-            uint4 qv[UNROLL], kv[UNROLL], vv[UNROLL];
+        float wt[8];
+        if constexpr (NORM) unpack8(*reinterpret_cast<const uint4 *>((tensor == 0 ? p.wq : p.wk) + c * 8), wt);
+        const float eps = tensor == 0 ? p.epsq : p.epsk;
 #pragma unroll
-            for (int u = 0; u < UNROLL; ++u) {
-                const int h = h0 + u * RPI + g;
-                if (h < H) {  // uniform over the LPR lanes of a row
-                    qv[u] = ld_nt(qsrc + h * D);
-                    if constexpr (HAS_K) kv[u] = ld_nt(ksrc + h * D);
-                    if constexpr (HAS_V) vv[u] = ld_nt(vsrc + h * D);
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < UNROLL; ++u) {
-                const int h = h0 + u * RPI + g;
-                if (h < H) {
-                    st_nt(qdst + h * D, norm_rope_chunk<LPR, NORM, ROPE>(qv[u], wq, p.epsq, f0, f1));
-                    if constexpr (HAS_K)
-                        st_nt(p.ok + (kv_row + h) * D + c * 8,
-                              norm_rope_chunk<LPR, NORM, ROPE>(kv[u], wk, p.epsk, f0, f1));
-                    if constexpr (HAS_V) st_nt(p.ov + (kv_row + h) * D + c * 8, vv[u]);
-                }
-            }
+        for (int u = 0; u < U; ++u) {
+            const int h = h0 + u * RPI;
+            if (FULL || h < H) st_nt(dst + (int64_t)h * D, norm_rope_chunk<LPR, NORM, ROPE>(x[u], wt, eps, f0, f1));
         }
-    } else if constexpr (HAS_V) {
+    } else if constexpr (NTENS == 3) {
         // Prefix copy: B * P * H rows of D, RPI rows per wave instruction.
         const int64_t gi = ((int64_t)blockIdx.x - p.main_blocks) * 256 + threadIdx.x;
         const int64_t row = gi / LPR;
         const int64_t PH = p.P * p.H;
-        const int64_t B = p.rows / (p.S * p.H);
+        const int64_t B = p.T / p.S;
         if (row >= B * PH) return;
         const int64_t bb = row / PH, within = row - bb * PH;
         const int64_t dst = (bb * (p.P + p.S) * p.H + within) * D + c * 8;
@@ -305,19 +389,41 @@ __global__ __launch_bounds__(256) void k_norm_rope(NormRopeArgs p) {
     }
 }
 
-template <bool NORM, bool ROPE, bool HAS_K, bool HAS_V>
-static int launch_norm_rope(NormRopeArgs a, int64_t D, int64_t B, hipStream_t st) {
-    const int64_t tokens = a.rows / a.H;   // one wave per token, 4 waves per workgroup
-    a.main_blocks = (tokens + 3) / 4;
-    const int64_t prefix_blocks = (HAS_V && a.P > 0) ? (B * a.P * a.H * (D / 8) + 255) / 256 : 0;
-    const int64_t blocks = a.main_blocks + prefix_blocks;
-    if (blocks >= (1ll << 31)) return fail(QIM_ERR_SHAPE, "norm/rope: too large");
-    dim3 grid((unsigned)blocks), block(256);
+template <int D, bool NORM, bool ROPE, int NTENS, int U, bool FULL>
+static void launch_norm_rope_shape(NormRopeArgs a, int64_t prefix_blocks, hipStream_t st) {
+    const int64_t rows_per_wave = U * (512 / D);
+    const int64_t groups = (a.H + rows_per_wave - 1) / rows_per_wave;
+    const int64_t waves = a.T * NTENS * groups;
+    a.groups = (uint32_t)groups;
+    a.main_waves = (uint32_t)waves;
+    a.main_blocks = (waves + 3) / 4;
+    hipLaunchKernelGGL((k_norm_rope<D, NORM, ROPE, NTENS, U, FULL>), dim3((unsigned)(a.main_blocks + prefix_blocks)),
+                       dim3(256), 0, st, a);
+}
+
+template <int D, bool NORM, bool ROPE, int NTENS>
+static void launch_norm_rope_d(const NormRopeArgs &a, int64_t prefix_blocks, hipStream_t st) {
+    constexpr int64_t RPI = 512 / D;
+    if (a.H % (3 * RPI) == 0) launch_norm_rope_shape<D, NORM, ROPE, NTENS, 3, true>(a, prefix_blocks, st);
+    else if (a.H % (4 * RPI) == 0) launch_norm_rope_shape<D, NORM, ROPE, NTENS, 4, true>(a, prefix_blocks, st);
+    else if (a.H % (2 * RPI) == 0) launch_norm_rope_shape<D, NORM, ROPE, NTENS, 2, true>(a, prefix_blocks, st);
+    else launch_norm_rope_shape<D, NORM, ROPE, NTENS, NR_ROWS, false>(a, prefix_blocks, st);
+}
+
+template <bool NORM, bool ROPE, int NTENS>
+static int launch_norm_rope(const NormRopeArgs &a, int64_t D, int64_t B, hipStream_t st) {
+    if (D != 64 && D != 128 && D != 256)
+        return fail(QIM_ERR_SHAPE, "norm/rope: head dim %lld not in {64, 128, 256}", (long long)D);
+    // The most waves any split launches (2 head rows per lane per wave).
+    const int64_t max_waves = a.T * NTENS * ((a.H + 2 * (512 / D) - 1) / (2 * (512 / D)));
+    const int64_t prefix_blocks = (NTENS == 3 && a.P > 0) ? (B * a.P * a.H * (D / 8) + 255) / 256 : 0;
+    if (max_waves >= (1ll << 31) || a.H >= (1ll << 30) || a.T >= (1ll << 31) ||
+        (max_waves + 3) / 4 + prefix_blocks >= (1ll << 31))
+        return fail(QIM_ERR_SHAPE, "norm/rope: too large (%lld tokens x %lld heads)", (long long)a.T, (long long)a.H);
     switch (D) {
-        case 64: hipLaunchKernelGGL((k_norm_rope<64, NORM, ROPE, HAS_K, HAS_V>), grid, block, 0, st, a); break;
-        case 128: hipLaunchKernelGGL((k_norm_rope<128, NORM, ROPE, HAS_K, HAS_V>), grid, block, 0, st, a); break;
-        case 256: hipLaunchKernelGGL((k_norm_rope<256, NORM, ROPE, HAS_K, HAS_V>), grid, block, 0, st, a); break;
-        default: return fail(QIM_ERR_SHAPE, "norm/rope: head dim %lld not in {64, 128, 256}", (long long)D);
+        case 64: launch_norm_rope_d<64, NORM, ROPE, NTENS>(a, prefix_blocks, st); break;
+        case 128: launch_norm_rope_d<128, NORM, ROPE, NTENS>(a, prefix_blocks, st); break;
+        default: launch_norm_rope_d<256, NORM, ROPE, NTENS>(a, prefix_blocks, st); break;
     }
     return QIM_OK;
 }
@@ -370,13 +476,10 @@ extern "C" int qim_rms_norm(const void *x, const void *w, void *out, int64_t row
     QIM_REQUIRE(rows > 0, QIM_ERR_SHAPE, "qim_rms_norm: empty input");
     QIM_REQUIRE(aligned16(x) && aligned16(w) && aligned16(out), QIM_ERR_LAYOUT,
                 "qim_rms_norm: operands must be 16-byte aligned");
-    // No table and no per-token state: view the rows as tokens of `heads` rows so
-    // that every lane group of the one-wave-per-token kernel has work.
-    const int64_t rpi = D > 0 ? 512 / (D > 512 ? 512 : D) : 1;  // 64 lanes x 8 values / D
-    const int64_t heads = (rpi > 0 && rows % rpi == 0) ? rpi : 1;
+    // No table and no per-token state: the rows are the heads of one token.
     NormRopeArgs a{(const uint16_t *)x, nullptr, nullptr, nullptr, nullptr, (const uint16_t *)w, nullptr,
-                   nullptr, (uint16_t *)out, nullptr, nullptr, rows, rows / heads, 0, heads, heads * D, eps, eps, 0};
-    int rc = launch_norm_rope<true, false, false, false>(a, D, 1, as_stream(stream));
+                   nullptr, (uint16_t *)out, nullptr, nullptr, 1, 1, 0, rows, rows * D, eps, eps, 0, 0, 0};
+    int rc = launch_norm_rope<true, false, 1>(a, D, 1, as_stream(stream));
     return rc ? rc : check_launch("qim_rms_norm");
 }
 
@@ -387,8 +490,9 @@ extern "C" int qim_rope_qk(const void *q, const void *k, const void *freqs, void
     QIM_REQUIRE(aligned16(q) && aligned16(k) && aligned16(freqs) && aligned16(oq) && aligned16(ok),
                 QIM_ERR_LAYOUT, "qim_rope_qk: operands must be 16-byte aligned");
     NormRopeArgs a{(const uint16_t *)q, (const uint16_t *)k, nullptr, nullptr, nullptr, nullptr, nullptr,
-                   (const float *)freqs, (uint16_t *)oq, (uint16_t *)ok, nullptr, B * S * H, S, 0, H, H * D, 0.f, 0.f, 0};
-    int rc = launch_norm_rope<false, true, true, false>(a, D, B, as_stream(stream));
+                   (const float *)freqs, (uint16_t *)oq, (uint16_t *)ok, nullptr, B * S, S, 0, H, H * D, 0.f, 0.f,
+                   0, 0, 0};
+    int rc = launch_norm_rope<false, true, 2>(a, D, B, as_stream(stream));
     return rc ? rc : check_launch("qim_rope_qk");
 }
 
@@ -408,8 +512,8 @@ extern "C" int qim_qk_norm_rope_pack(const void *q, const void *k, const void *v
         QIM_REQUIRE(!pp || aligned16(pp), QIM_ERR_LAYOUT, "qim_qk_norm_rope_pack: operands must be 16-byte aligned");
     NormRopeArgs a{(const uint16_t *)q, (const uint16_t *)k, (const uint16_t *)v, (const uint16_t *)ck,
                    (const uint16_t *)cv, (const uint16_t *)wq, (const uint16_t *)wk, (const float *)freqs,
-                   (uint16_t *)oq, (uint16_t *)ok, (uint16_t *)ov, B * S * H, S, P, H, ldt, epsq, epsk, 0};
-    int rc = v ? launch_norm_rope<true, true, true, true>(a, D, B, as_stream(stream))
-               : launch_norm_rope<true, true, true, false>(a, D, B, as_stream(stream));
+                   (uint16_t *)oq, (uint16_t *)ok, (uint16_t *)ov, B * S, S, P, H, ldt, epsq, epsk, 0, 0, 0};
+    int rc = v ? launch_norm_rope<true, true, 3>(a, D, B, as_stream(stream))
+               : launch_norm_rope<true, true, 2>(a, D, B, as_stream(stream));
     return rc ? rc : check_launch("qim_qk_norm_rope_pack");
 }

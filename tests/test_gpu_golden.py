@@ -1,7 +1,9 @@
 """HIP kernels against the committed golden fixtures (tests/golden/golden.npz):
-bit-exact for MXFP8 bytes, the gated residual and RoPE; within the bf16 chain
-tolerance for the normalisations and SwiGLU; GEMM within rel-Frobenius 1e-2
-of the dequantize-then-matmul."""
+bit-exact against the oracle's outputs for MXFP8 bytes, the gated residual,
+RoPE and the normalisations (float64 row statistics rounded once); within the
+bf16 chain tolerance against eager torch-CPU outputs (own fp32 reductions) and
+for SwiGLU (device exp); GEMM within rel-Frobenius 1e-2 of the
+dequantize-then-matmul."""
 import os
 
 import numpy as np
@@ -47,17 +49,17 @@ def test_quantize(dev, tag):
 @pytest.mark.parametrize("mag", ["0.001", "1", "20"])
 def test_layer_norm_scale(dev, mag):
     out = layernorm.layer_norm_scale(t(f"ln_{mag}_x", dev), t(f"ln_{mag}_scale", dev), _LN(512))
-    assert bf16_close_chain(bits(out), G[f"ln_{mag}_oracle"])[0]
+    assert np.array_equal(bits(out), G[f"ln_{mag}_oracle"])
     assert bf16_close_chain(bits(out), G[f"ln_{mag}_eager"])[0]
 
 
 def test_adaln_chain_and_quantize(dev):
     x, s, sh, g, r = (t(f"adaln_{n}", dev) for n in ("x", "scale", "shift", "gate", "res"))
     out = layernorm.layer_norm_scale(x, s, _LN(512), shift=sh, gate=g, residual=r, add_one=True)
-    assert bf16_close_chain(bits(out), G["adaln_oracle"])[0]
+    assert np.array_equal(bits(out), G["adaln_oracle"])
     q = epilogue.layer_norm_scale_quantize(x, s, _LN(512), shift=sh, gate=g, residual=r, add_one=True)
-    assert (u8(q.values) != G["adaln_q_oracle"]).mean() < 1e-3
-    assert (u8(q.scales) != G["adaln_s_oracle"]).mean() < 1e-3
+    assert np.array_equal(u8(q.values), G["adaln_q_oracle"])
+    assert np.array_equal(u8(q.scales), G["adaln_s_oracle"])
 
 
 def test_residual(dev):
@@ -84,10 +86,8 @@ def test_prepare_attention_inputs(dev):
     oq, ok, ov = attention.prepare_attention_inputs(a("q"), a("k"), a("v"), _RMS(a("wq")), _RMS(a("wk")), f,
                                                     a("ck"), a("cv"))
     assert np.array_equal(bits(ov), G["attn_ov_oracle"])
-    assert rel_fro(bits(oq).astype(np.float64), G["attn_oq_oracle"].astype(np.float64)) < 1  # same scale
-    from oracle import oracle as O
-    for got, ref in ((bits(oq), G["attn_oq_oracle"]), (bits(ok), G["attn_ok_oracle"])):
-        assert rel_fro(O.bf16_to_f32(got), O.bf16_to_f32(ref)) < 4e-3
+    assert np.array_equal(bits(oq), G["attn_oq_oracle"])
+    assert np.array_equal(bits(ok), G["attn_ok_oracle"])
 
 
 def test_gemm(dev):
