@@ -50,13 +50,12 @@ struct GemmArgs {
     int64_t ldo;
     uint8_t *out_scales;
     int tiles_m, tiles_n;
+    int main_tiles;  // whole tiles; workgroups past them compute quarter tiles of the rest
 };
 
 __device__ __forceinline__ int kswz(int row) { return ((row >> 1) ^ (row >> 2)) & 3; }
 // LDS byte offset of logical 16-byte chunk c of tile row `row` (64-byte rows).
 __device__ __forceinline__ int lds_off(int row, int c) { return row * BK + ((c ^ kswz(row)) << 4); }
-// Offset of the scale dword of local row r (0..255) inside a 1 KiB scale tile.
-__device__ __forceinline__ int scale_dword(int r) { return (r >> 7) * 512 + (r & 31) * 16 + ((r & 127) >> 5) * 4; }
 
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -141,7 +140,7 @@ __device__ __forceinline__ void issue_stage(const GemmArgs &p, const LoadPlan &L
 
 struct Frags {
     i32x8_t a[4], b[4];
-    uint32_t sa[4], sb[4];
+    uint4 sa, sb;  // scale dwords of row tiles 0..3 (exponents of the 128-K group's 4 blocks)
 };
 
 // Fragment reads of one ring slot (stage), one operand tile at a time.
@@ -150,8 +149,12 @@ __device__ __forceinline__ i32x8_t read_tile(const uint8_t *base, int row, int k
     const uint4 hi = *reinterpret_cast<const uint4 *>(base + lds_off(row, 2 + kh));
     return i32x8_t{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
 }
-__device__ __forceinline__ uint32_t read_scale(const uint8_t *base, int row) {
-    return *reinterpret_cast<const uint32_t *>(base + scale_dword(row));
+// The four scale dwords of a wave's row tiles t = 0..3 (local rows
+// r = h*128 + t*32 + lr of a 1 KiB scale tile, whose dword for row r sits at
+// (r/128)*512 + (r%32)*16 + ((r%128)/32)*4 = h*512 + lr*16 + t*4): contiguous,
+// so one 16-byte read.
+__device__ __forceinline__ uint4 read_scales(const uint8_t *base, int h, int lr) {
+    return *reinterpret_cast<const uint4 *>(base + h * 512 + lr * 16);
 }
 
 __device__ __forceinline__ void read_frags(const uint8_t *slot, int wm, int wn, int lr, int kh, Frags &f) {
@@ -159,9 +162,9 @@ __device__ __forceinline__ void read_frags(const uint8_t *slot, int wm, int wn, 
     for (int t = 0; t < 4; ++t) {
         f.a[t] = read_tile(slot, wm * 128 + t * 32 + lr, kh);
         f.b[t] = read_tile(slot + TILE_BYTES, wn * 128 + t * 32 + lr, kh);
-        f.sa[t] = read_scale(slot + 2 * TILE_BYTES, wm * 128 + t * 32 + lr);
-        f.sb[t] = read_scale(slot + 2 * TILE_BYTES + SCALE_BYTES, wn * 128 + t * 32 + lr);
     }
+    f.sa = read_scales(slot + 2 * TILE_BYTES, wm, lr);
+    f.sb = read_scales(slot + 2 * TILE_BYTES + SCALE_BYTES, wn, lr);
 }
 
 // Every stage issues its 10 loads unconditionally (past the end of K they
@@ -188,10 +191,11 @@ __device__ __forceinline__ void pipeline_step(const GemmArgs &p, const LoadPlan 
                                               f32x16_t (&acc)[4][4], const Frags &cur, Frags &nxt, int wm,
                                               int wn, int lr, int kh) {
     int sa[4], sb[4];
+    const uint32_t ca[4] = {cur.sa.x, cur.sa.y, cur.sa.z, cur.sa.w}, cb[4] = {cur.sb.x, cur.sb.y, cur.sb.z, cur.sb.w};
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-        sa[t] = (int)(cur.sa[t] >> (8 * kh));
-        sb[t] = (int)(cur.sb[t] >> (8 * kh));
+        sa[t] = (int)(ca[t] >> (8 * kh));
+        sb[t] = (int)(cb[t] >> (8 * kh));
     }
 #define QIM_MF(i, j)                                                                                          \
     acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(cur.a[i], cur.b[j], acc[i][j], 0, 0, PAR * 2, \
@@ -213,12 +217,12 @@ __device__ __forceinline__ void pipeline_step(const GemmArgs &p, const LoadPlan 
     block_barrier();
     QIM_SCHED();
     QIM_STEP(0, 1, dma16(p.aq, L.a[0] + kofs, fb + (w4 + 0) * 1024));
+    // The next stage's scales: the same 128-K group after an even stage (kept
+    // in registers), a new group after an odd one (one 16-byte read each).
     QIM_STEP(0, 2, dma16(p.aq, L.a[1] + kofs, fb + (w4 + 1) * 1024);
-             nxt.sa[0] = read_scale(nsa, ra0); nxt.sa[1] = read_scale(nsa, ra0 + 32);
-             nxt.sa[2] = read_scale(nsa, ra0 + 64); nxt.sa[3] = read_scale(nsa, ra0 + 96));
+             if constexpr (PAR == 0) nxt.sa = cur.sa; else nxt.sa = read_scales(nsa, wm, lr));
     QIM_STEP(0, 3, dma16(p.aq, L.a[2] + kofs, fb + (w4 + 2) * 1024);
-             nxt.sb[0] = read_scale(nsb, rb0); nxt.sb[1] = read_scale(nsb, rb0 + 32);
-             nxt.sb[2] = read_scale(nsb, rb0 + 64); nxt.sb[3] = read_scale(nsb, rb0 + 96));
+             if constexpr (PAR == 0) nxt.sb = cur.sb; else nxt.sb = read_scales(nsb, wn, lr));
     QIM_STEP(1, 0, dma16(p.aq, L.a[3] + kofs, fb + (w4 + 3) * 1024); nxt.a[0] = read_tile(next, ra0, kh));
     QIM_STEP(1, 1, dma16(p.bq, L.b[0] + kofs, fb + TILE_BYTES + (w4 + 0) * 1024);
              nxt.b[0] = read_tile(next + TILE_BYTES, rb0, kh));
@@ -242,15 +246,10 @@ __device__ __forceinline__ void pipeline_step(const GemmArgs &p, const LoadPlan 
 #undef QIM_MF
 }
 
-// Workgroup -> tile.  Workgroups are dispatched round-robin over the 8 XCDs,
-// so workgroup w runs on XCD w % 8; tile ids are remapped so that each XCD
-// owns one contiguous range, walked in groups of 4 tile-rows (column-major
-// inside a group) so the tiles resident on one XCD share A rows and B columns
-// in that XCD's L2.
-__device__ __forceinline__ void tile_of(const GemmArgs &p, int &tm, int &tn) {
-    const int nt = p.tiles_m * p.tiles_n;
-    int t = blockIdx.x;
-    if ((nt & 7) == 0) t = (t & 7) * (nt >> 3) + (t >> 3);
+// Tile id -> (tile row, tile column): groups of 4 tile-rows, column-major
+// inside a group, so consecutive tiles share B columns and, within a group, A
+// rows in L2.
+__device__ __forceinline__ void tile_coords(const GemmArgs &p, int t, int &tm, int &tn) {
     constexpr int GM = 4;
     const int per_group = GM * p.tiles_n;
     const int group = t / per_group, first = group * GM;
@@ -258,6 +257,18 @@ __device__ __forceinline__ void tile_of(const GemmArgs &p, int &tm, int &tn) {
     const int r = t - group * per_group;
     tm = first + r % gm;
     tn = r / gm;
+}
+
+// Workgroup -> tile.  Workgroups are dispatched round-robin over the 8 XCDs,
+// so workgroup w runs on XCD w % 8; tile ids are remapped so that each XCD
+// owns one contiguous range, walked in groups of 4 tile-rows (column-major
+// inside a group) so the tiles resident on one XCD share A rows and B columns
+// in that XCD's L2.
+__device__ __forceinline__ void tile_of(const GemmArgs &p, int &tm, int &tn) {
+    const int nt = p.main_tiles;
+    int t = blockIdx.x;
+    if ((nt & 7) == 0) t = (t & 7) * (nt >> 3) + (t >> 3);
+    tile_coords(p, t, tm, tn);
 }
 
 // ------------------------------------------------------------- epilogue --
@@ -271,29 +282,29 @@ __device__ __forceinline__ void tile_of(const GemmArgs &p, int &tm, int &tn) {
 //     loads, or MXFP8 quantization of 32-column blocks = 4 lanes) before one
 //     16-byte (8-byte for codes) store.
 // Accumulator i of MFMA tile (ti, tj) is row 32ti + 8(i/4) + 4(l/32) + i%4,
-// column 32tj + l%32 of the wave's block.  Row stride 2W + 16 bytes (W = 128
-// or 64 output columns) keeps both passes free of bank conflicts.
-template <int EPI>
-__device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[4][4], uint8_t *lds, int wm, int wn,
-                                         int64_t m0, int64_t n0, int lane) {
+// column 32tj + l%32 of the wave's block of TI x TJ MFMA tiles, whose first
+// row is row0 and first GEMM column gcol0.  Row stride 2W + 16 bytes
+// (W = 32 TJ output columns, half of that for SwiGLU) keeps both passes free
+// of bank conflicts.
+template <int EPI, int TI, int TJ>
+__device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][TJ], uint8_t *lds, int64_t row0,
+                                         int64_t gcol0, int lane, int wave) {
     constexpr bool SWI = EPI == QIM_EPI_SWIGLU || EPI == QIM_EPI_SWIGLU_QUANT;
-    constexpr int W = SWI ? 64 : 128;        // output columns of this wave
-    constexpr int RS = 2 * W + 16;           // LDS row stride (bytes)
-    constexpr int LPR = W / 8;               // lanes per row in pass 2
-    constexpr int RPI = 64 / LPR;            // rows per pass-2 instruction
+    constexpr int W = SWI ? 16 * TJ : 32 * TJ;  // output columns of this wave
+    constexpr int RS = 2 * W + 16;              // LDS row stride (bytes)
+    constexpr int LPR = W / 8;                  // lanes per row in pass 2
+    constexpr int RPI = 64 / LPR;               // rows per pass-2 instruction
     const int lr = lane & 31, kh = lane >> 5;
-    const int wave = threadIdx.x >> 6;
     uint8_t *reg = lds + wave * (64 * RS);
-    const int64_t row0 = m0 + wm * 128;
-    const int64_t col0 = SWI ? (n0 + wn * 128) / 2 : n0 + wn * 128;  // first output column
+    const int64_t col0 = SWI ? gcol0 / 2 : gcol0;  // first output column
     const int64_t F = p.N / 2;
-    float bias[4] = {0.f, 0.f, 0.f, 0.f};
+    float bias[TJ] = {};
     if constexpr (EPI == QIM_EPI_BIAS) {
 #pragma unroll
-        for (int tj = 0; tj < 4; ++tj) bias[tj] = bf16_to_f32(p.bias[n0 + wn * 128 + tj * 32 + lr]);
+        for (int tj = 0; tj < TJ; ++tj) bias[tj] = bf16_to_f32(p.bias[gcol0 + tj * 32 + lr]);
     }
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
+    for (int half = 0; half < TI / 2; ++half) {
         // pass 1
 #pragma unroll
         for (int tl = 0; tl < 2; ++tl) {
@@ -304,13 +315,13 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[4][4
                 uint16_t *rowp = reinterpret_cast<uint16_t *>(reg + r * RS);
                 if constexpr (SWI) {
 #pragma unroll
-                    for (int u = 0; u < 2; ++u) {
+                    for (int u = 0; u < TJ / 2; ++u) {
                         const float y = swiglu1(rbf(acc[ti][2 * u][i]), rbf(acc[ti][2 * u + 1][i]));
                         rowp[u * 32 + lr] = (uint16_t)(pack_bf16x2(y, 0.0f) & 0xffffu);
                     }
                 } else {
 #pragma unroll
-                    for (int tj = 0; tj < 4; ++tj) {
+                    for (int tj = 0; tj < TJ; ++tj) {
                         float v = acc[ti][tj][i];
                         if constexpr (EPI == QIM_EPI_BIAS) v = v + bias[tj];
                         rowp[tj * 32 + lr] = (uint16_t)(pack_bf16x2(v, 0.0f) & 0xffffu);
@@ -359,9 +370,149 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[4][4
     }
 }
 
+
+// ------------------------------------------------------------ tail tiles --
+// The tile grid is rarely a whole number of rounds of the CUs (4352 x 12288:
+// 816 tiles = 3.19 rounds of 256).  The last r tiles (r <= CUs / 2) are then
+// computed as 4r quarter tiles of 128 x 128 by as many extra workgroups, so
+// the last round takes about a quarter of a tile's time instead of a whole
+// one.  A quarter tile: 4 waves in a 2 x 2 grid, each a 64 x 64 block of 2 x 2
+// MFMA tiles, on the same 4-stage LDS ring (half of each operand area used)
+// with the same schedule rules.
+constexpr int QLOADS = 5;  // per wave per stage: 2 A + 2 B (16 B) + 1 scale (4 B)
+
+struct QPlan {
+    uint32_t a[2], b[2];   // byte offsets into aq / bq (stage 0)
+    uint32_t sc;           // byte offset of this wave's 256 scale bytes (stage 0)
+    const uint8_t *sc_base;
+    int wave;
+};
+
+__device__ __forceinline__ QPlan make_qplan(const GemmArgs &p, int64_t m0, int64_t n0) {
+    QPlan Q;
+    const int lane = threadIdx.x & 63;
+    Q.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int row = (Q.wave * 2 + j) * 16 + (lane >> 2);
+        const int c = (lane & 3) ^ kswz(row);
+        int64_t ar = m0 + row;
+        ar = ar < p.Mp ? ar : p.Mp - 1;
+        Q.a[j] = (uint32_t)(ar * p.K + c * 16);
+        Q.b[j] = (uint32_t)((n0 + row) * p.K + c * 16);
+    }
+    // Waves 0, 1 load the A scale chunk of rows [m0, m0 + 128), waves 2, 3 the B chunk.
+    const int64_t kt = p.K / 128;
+    const int64_t grow = Q.wave < 2 ? m0 / 128 : n0 / 128;
+    Q.sc_base = Q.wave < 2 ? p.as : p.bs;
+    Q.sc = (uint32_t)(grow * kt * 512 + (Q.wave & 1) * 256 + lane * 4);
+    return Q;
+}
+
+__device__ __forceinline__ void issue_qstage(const GemmArgs &p, const QPlan &Q, uint8_t *slot, int s) {
+    const uint32_t kofs = (uint32_t)s * BK, base = lds_addr(slot), w2 = Q.wave * 2;
+    dma16(p.aq, Q.a[0] + kofs, base + (w2 + 0) * 1024);
+    dma16(p.aq, Q.a[1] + kofs, base + (w2 + 1) * 1024);
+    dma16(p.bq, Q.b[0] + kofs, base + TILE_BYTES + (w2 + 0) * 1024);
+    dma16(p.bq, Q.b[1] + kofs, base + TILE_BYTES + (w2 + 1) * 1024);
+    dma4(Q.sc_base, Q.sc + (uint32_t)(s >> 1) * 512,
+         base + 2 * TILE_BYTES + (Q.wave < 2 ? 0 : SCALE_BYTES) + (Q.wave & 1) * 256);
+}
+
+struct QFrags {
+    i32x8_t a[2], b[2];
+    uint2 sa, sb;  // scale dwords of row tiles 0, 1
+};
+
+// Rows h*64 + t*32 + lr (t = 0, 1) of a 128-row scale chunk: dwords at
+// lr*16 + (2h + t)*4, contiguous.
+__device__ __forceinline__ uint2 read_qscales(const uint8_t *base, int h, int lr) {
+    return *reinterpret_cast<const uint2 *>(base + lr * 16 + h * 8);
+}
+
+__device__ __forceinline__ void read_qfrags(const uint8_t *slot, int wm, int wn, int lr, int kh, QFrags &f, bool scales) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        f.a[t] = read_tile(slot, wm * 64 + t * 32 + lr, kh);
+        f.b[t] = read_tile(slot + TILE_BYTES, wn * 64 + t * 32 + lr, kh);
+    }
+    if (scales) {
+        f.sa = read_qscales(slot + 2 * TILE_BYTES, wm, lr);
+        f.sb = read_qscales(slot + 2 * TILE_BYTES + SCALE_BYTES, wn, lr);
+    }
+}
+
+template <int PAR>
+__device__ __forceinline__ void qstep(const GemmArgs &p, const QPlan &Q, uint8_t *lds, int s, int S,
+                                      f32x16_t (&acc)[2][2], const QFrags &cur, QFrags &nxt, int wm, int wn, int lr,
+                                      int kh) {
+    const int sa[2] = {(int)(cur.sa.x >> (8 * kh)), (int)(cur.sa.y >> (8 * kh))};
+    const int sb[2] = {(int)(cur.sb.x >> (8 * kh)), (int)(cur.sb.y >> (8 * kh))};
+#define QIM_QMF(i, j)                                                                                          \
+    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(cur.a[i], cur.b[j], acc[i][j], 0, 0, PAR * 2, \
+                                                                sa[i], PAR * 2, sb[j])
+    QIM_QMF(0, 0);
+    QIM_SCHED();
+    wait_vmcnt<2 * QLOADS>();
+    block_barrier();
+    QIM_SCHED();
+    issue_qstage(p, Q, lds + (s & 3) * STAGE_BYTES, s + 4 < S ? s + 4 : S - 1);
+    QIM_SCHED();
+    QIM_QMF(0, 1);
+    QIM_SCHED();
+    if constexpr (PAR == 0) {
+        read_qfrags(lds + ((s + 1) & 3) * STAGE_BYTES, wm, wn, lr, kh, nxt, false);
+        nxt.sa = cur.sa;
+        nxt.sb = cur.sb;
+    } else {
+        read_qfrags(lds + ((s + 1) & 3) * STAGE_BYTES, wm, wn, lr, kh, nxt, true);
+    }
+    QIM_SCHED();
+    QIM_QMF(1, 0);
+    QIM_QMF(1, 1);
+    QIM_SCHED();
+#undef QIM_QMF
+}
+
+template <int EPI>
+__device__ __forceinline__ void quarter_tile(const GemmArgs &p, uint8_t *lds, int q) {
+    const int tile = p.main_tiles + q / 4, quarter = q & 3;
+    int tm, tn;
+    tile_coords(p, tile, tm, tn);
+    const int64_t m0 = (int64_t)tm * BM + (quarter >> 1) * 128, n0 = (int64_t)tn * BN + (quarter & 1) * 128;
+    if (m0 >= p.Mp) return;  // padding rows only (whole workgroup)
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1, lr = lane & 31, kh = lane >> 5;
+    const int S = (int)(p.K / BK);
+    f32x16_t acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = f32x16_t{};
+    const QPlan Q = make_qplan(p, m0, n0);
+#pragma unroll
+    for (int i = 0; i < NSTAGE; ++i) issue_qstage(p, Q, lds + i * STAGE_BYTES, i < S ? i : S - 1);
+    wait_vmcnt<3 * QLOADS>();  // stage 0 landed
+    block_barrier();
+    QFrags fa, fb;
+    read_qfrags(lds, wm, wn, lr, kh, fa, true);
+    for (int s = 0; s < S; s += 2) {
+        qstep<0>(p, Q, lds, s, S, acc, fa, fb, wm, wn, lr, kh);
+        qstep<1>(p, Q, lds, s + 1, S, acc, fb, fa, wm, wn, lr, kh);
+    }
+    wait_vmcnt<0>();
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    block_barrier();
+    epilogue<EPI, 2, 2>(p, acc, lds, m0 + wm * 64, n0 + wn * 64, lane, wave);
+}
+
 template <int EPI>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_mx_gemm(GemmArgs p) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
+    if ((int)blockIdx.x >= p.main_tiles) {  // a quarter tile of the last partial round
+        quarter_tile<EPI>(p, lds, (int)blockIdx.x - p.main_tiles);
+        return;
+    }
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     int tm, tn;
@@ -393,7 +544,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     block_barrier();
 
-    epilogue<EPI>(p, acc, lds, wm, wn, m0, n0, lane);
+    epilogue<EPI, 4, 4>(p, acc, lds, m0 + wm * 128, n0 + wn * 128, lane, wave);
+}
+
+// Compute units of the current device, cached per device (0 if unknown).
+static int device_cus() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+    if (dev < 64 && cached[dev]) return cached[dev];
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    if (dev < 64) cached[dev] = n;
+    return n;
+}
+
+// Whole tiles to launch: all of them, or all but the last r when the last
+// round of the CUs would hold r <= CUs / 2 tiles (those become 4r quarters).
+static int64_t main_tile_count(int64_t tiles) {
+    const int64_t cus = device_cus();
+    if (cus <= 0 || tiles <= cus) return tiles;
+    const int64_t r = tiles % cus;
+    return (r > 0 && 2 * r <= cus) ? tiles - r : tiles;
 }
 
 template <int EPI>
@@ -407,7 +579,8 @@ static int launch_gemm(const GemmArgs &a, int64_t tiles, hipStream_t st) {
                         hipGetErrorString(e));
         configured = true;
     }
-    hipLaunchKernelGGL(k_mx_gemm<EPI>, dim3((unsigned)tiles), dim3(256), LDS_BYTES, st, a);
+    const int64_t grid = a.main_tiles + 4 * (tiles - a.main_tiles);
+    hipLaunchKernelGGL(k_mx_gemm<EPI>, dim3((unsigned)grid), dim3(256), LDS_BYTES, st, a);
     return QIM_OK;
 }
 
@@ -424,7 +597,7 @@ extern "C" int qim_mxfp8_gemm(const void *aq, const void *as, const void *bq, co
     QIM_REQUIRE(N % BN == 0, QIM_ERR_SHAPE, "qim_mxfp8_gemm: N=%lld is not a multiple of 256", (long long)N);
     const int64_t Mp = (M + 127) / 128 * 128;
     const int64_t tiles_m = (Mp + BM - 1) / BM, tiles_n = N / BN;
-    QIM_REQUIRE(tiles_m * tiles_n < (1ll << 31), QIM_ERR_SHAPE, "qim_mxfp8_gemm: too many tiles");
+    QIM_REQUIRE(4 * tiles_m * tiles_n < (1ll << 31), QIM_ERR_SHAPE, "qim_mxfp8_gemm: too many tiles");
     QIM_REQUIRE(aligned16(aq) && aligned16(bq) && aligned16(as) && aligned16(bs) && aligned16(out) &&
                     (!res || aligned16(res)) && (!gate || aligned16(gate)) && (!out_scales || aligned16(out_scales)),
                 QIM_ERR_LAYOUT, "qim_mxfp8_gemm: operands must be 16-byte aligned");
@@ -434,8 +607,9 @@ extern "C" int qim_mxfp8_gemm(const void *aq, const void *as, const void *bq, co
                 "qim_mxfp8_gemm: operands above 2 GiB are not supported");
     GemmArgs a{(const uint8_t *)aq, (const uint8_t *)as, (const uint8_t *)bq, (const uint8_t *)bs, M, Mp, N, K,
                (const uint16_t *)bias, (const uint16_t *)gate, (const uint16_t *)res, seq > 0 ? seq : M, out, ldo,
-               (uint8_t *)out_scales, (int)tiles_m, (int)tiles_n};
+               (uint8_t *)out_scales, (int)tiles_m, (int)tiles_n, 0};
     const int64_t tiles = tiles_m * tiles_n;
+    a.main_tiles = (int)main_tile_count(tiles);
     int rc;
     switch (epilogue) {
         case QIM_EPI_NONE:

@@ -499,3 +499,47 @@ def test_mxfp8_gemm_swiglu_epilogues(dev):
     sep = mxfp8.quantize(y)
     assert yq.rows == m and np.array_equal(u8(yq.values), u8(sep.values))
     assert np.array_equal(u8(yq.scales), u8(sep.scales))
+
+
+@pytest.mark.parametrize("m,n,k", [(4352, 4096, 512), (4200, 4096, 384)])
+@pytest.mark.parametrize("epi", ["none", "bias", "gated_residual", "swiglu", "swiglu_quant"])
+def test_mxfp8_gemm_tail_quarter_tiles(dev, m, n, k, epi):
+    """272 tiles on 256 CUs: the last 16 (tile row 16, rows >= 4096) run as
+    128 x 128 quarter tiles (with M = 4200 the bottom quarters are padding).
+    Every epilogue against the oracle on rows of both kinds of tile."""
+    g = torch.Generator().manual_seed(6)
+    a = bf16_randn(g, (m, k))
+    w = bf16_randn(g, (n, k), 0.05)
+    say("gemm tail", m, n, k, epi)
+    aq = mxfp8.quantize(a.to(dev))
+    wq = mxfp8.quantize(w.to(dev))
+    rows = np.concatenate([np.random.default_rng(2).choice(4096, 12, replace=False),
+                           np.arange(4096, m, 17), [m - 1]])
+    acc = O.mx_gemm(u8(aq.values), u8(aq.scales), u8(wq.values), u8(wq.scales), rows=rows)
+    kw, ref = {}, None
+    if epi == "bias":
+        kw["bias"] = bf16_randn(g, (n,), 0.01).to(dev)
+        ref = acc + bf16_values(bits(kw["bias"].cpu()))[None, :]
+    elif epi == "gated_residual":
+        res, gate = bf16_randn(g, (m, n)), bf16_randn(g, (2, 1, n)).tanh()
+        kw.update(residual=res.to(dev), gate=gate.to(dev), seq=m // 2)
+        proj = bf16_values(O.f32_to_bf16(acc))
+        ref = bf16_values(bits(res))[rows] + bf16_values(bits(gate)).reshape(2, n)[rows // (m // 2)] * proj
+    elif epi in ("swiglu", "swiglu_quant"):
+        f = n // 2
+        accg = acc.reshape(len(rows), f // 32, 2, 32)[:, :, 0].reshape(len(rows), f)
+        accu = acc.reshape(len(rows), f // 32, 2, 32)[:, :, 1].reshape(len(rows), f)
+        ref = bf16_values(O.swiglu(O.f32_to_bf16(accg), O.f32_to_bf16(accu)))
+    else:
+        ref = acc
+    y = gemm.mx_matmul(aq, wq.values, wq.scales, epilogue=epi, **kw)
+    if epi == "swiglu_quant":
+        yb = gemm.mx_matmul(aq, wq.values, wq.scales, epilogue="swiglu")
+        sep = mxfp8.quantize(yb)
+        assert y.rows == m and np.array_equal(u8(y.values), u8(sep.values))
+        assert np.array_equal(u8(y.scales), u8(sep.scales))
+        y = yb
+    got = bf16_values(bits(y))[rows]
+    assert rel_fro(got, ref) < 1e-2
+    for part in (rows < 4096, rows >= 4096):
+        assert rel_fro(got[part], ref[part]) < 1e-2
