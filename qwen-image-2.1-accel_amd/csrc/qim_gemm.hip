@@ -272,30 +272,37 @@ __device__ __forceinline__ void tile_of(const GemmArgs &p, int &tm, int &tn) {
 }
 
 // ------------------------------------------------------------- epilogue --
-// Two passes per half of the wave's 128 rows, through a wave-private LDS
-// region (the ring is free once the main loop has drained):
-//  1. registers -> LDS: each accumulator goes through the per-element part of
-//     the epilogue (bias add, or SwiGLU of the gate/up tile pair) and is
-//     stored as bf16 at its (row, column);
-//  2. LDS -> global: each lane reads 8 consecutive bf16 of a row (16 bytes)
-//     and applies the per-row part (gated residual with coalesced res/gate
-//     loads, or MXFP8 quantization of 32-column blocks = 4 lanes) before one
-//     16-byte (8-byte for codes) store.
+// Two passes per 64 rows (two MFMA row tiles) of the wave's block, through a
+// wave-private LDS region (the ring is free once the main loop has drained):
+//  1. registers -> LDS: the per-element part of the epilogue (bias add, or
+//     SwiGLU of the gate/up tile pair), then bf16.  Accumulators i = 4g'..4g'+3
+//     of an MFMA tile are 4 consecutive rows of one column, so they are packed
+//     two rows per dword (v_cvt_pk_bf16_f32) and stored with one 8-byte write:
+//     the region holds, per group of 4 rows and per column, the column's 4
+//     values (8 bytes).
+//  2. LDS -> global: each lane reads the 4 x 8 block of 4 rows x 8 columns
+//     (4 x 16 bytes), regroups it into the 4 rows' 16-byte vectors with byte
+//     permutes, applies the per-row part (gated residual with coalesced
+//     res/gate loads, or MXFP8 quantization of 32-column blocks = 4 lanes) and
+//     stores each row vector (8 bytes for codes).
 // Accumulator i of MFMA tile (ti, tj) is row 32ti + 8(i/4) + 4(l/32) + i%4,
 // column 32tj + l%32 of the wave's block of TI x TJ MFMA tiles, whose first
-// row is row0 and first GEMM column gcol0.  Row stride 2W + 16 bytes
-// (W = 32 TJ output columns, half of that for SwiGLU) keeps both passes free
-// of bank conflicts.
+// row is row0 and first GEMM column gcol0.  Within a row group, column c sits
+// at 8c + 16(c/8) bytes: the pass-2 lanes of a 16-lane read group start 80
+// bytes apart, on disjoint banks.
+template <int W>
+__device__ __forceinline__ int epi_col_offset(int c) { return c * 8 + (c >> 3) * 16; }
+
 template <int EPI, int TI, int TJ>
 __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][TJ], uint8_t *lds, int64_t row0,
                                          int64_t gcol0, int lane, int wave) {
     constexpr bool SWI = EPI == QIM_EPI_SWIGLU || EPI == QIM_EPI_SWIGLU_QUANT;
     constexpr int W = SWI ? 16 * TJ : 32 * TJ;  // output columns of this wave
-    constexpr int RS = 2 * W + 16;              // LDS row stride (bytes)
-    constexpr int LPR = W / 8;                  // lanes per row in pass 2
-    constexpr int RPI = 64 / LPR;               // rows per pass-2 instruction
+    constexpr int RGS = W * 8 + (W / 8) * 16;   // bytes per group of 4 rows
+    constexpr int LPR = W / 8;                  // lanes per row group in pass 2
+    constexpr int GPI = 64 / LPR;               // row groups per pass-2 step
     const int lr = lane & 31, kh = lane >> 5;
-    uint8_t *reg = lds + wave * (64 * RS);
+    uint8_t *reg = lds + wave * (16 * RGS);
     const int64_t col0 = SWI ? gcol0 / 2 : gcol0;  // first output column
     const int64_t F = p.N / 2;
     float bias[TJ] = {};
@@ -310,66 +317,93 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
         for (int tl = 0; tl < 2; ++tl) {
             const int ti = half * 2 + tl;
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int r = tl * 32 + 8 * (i >> 2) + 4 * kh + (i & 3);
-                uint16_t *rowp = reinterpret_cast<uint16_t *>(reg + r * RS);
+            for (int ig = 0; ig < 4; ++ig) {
+                uint8_t *grp = reg + (tl * 8 + ig * 2 + kh) * RGS;  // rows 32tl + 8ig + 4kh + 0..3
                 if constexpr (SWI) {
 #pragma unroll
                     for (int u = 0; u < TJ / 2; ++u) {
-                        const float y = swiglu1(rbf(acc[ti][2 * u][i]), rbf(acc[ti][2 * u + 1][i]));
-                        rowp[u * 32 + lr] = (uint16_t)(pack_bf16x2(y, 0.0f) & 0xffffu);
+                        float y[4];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            y[e] = swiglu1(rbf(acc[ti][2 * u][4 * ig + e]), rbf(acc[ti][2 * u + 1][4 * ig + e]));
+                        *reinterpret_cast<uint2 *>(grp + epi_col_offset<W>(u * 32 + lr)) =
+                            make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
                     }
                 } else {
 #pragma unroll
                     for (int tj = 0; tj < TJ; ++tj) {
-                        float v = acc[ti][tj][i];
-                        if constexpr (EPI == QIM_EPI_BIAS) v = v + bias[tj];
-                        rowp[tj * 32 + lr] = (uint16_t)(pack_bf16x2(v, 0.0f) & 0xffffu);
+                        float y[4];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            y[e] = acc[ti][tj][4 * ig + e];
+                            if constexpr (EPI == QIM_EPI_BIAS) y[e] = y[e] + bias[tj];
+                        }
+                        *reinterpret_cast<uint2 *>(grp + epi_col_offset<W>(tj * 32 + lr)) =
+                            make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
                     }
                 }
             }
         }
         // pass 2 (LDS operations of one wave complete in order: no wait needed)
-        const int cl = lane % LPR, rl = lane / LPR;
+        const int cl = lane % LPR, gl = lane / LPR;
 #pragma unroll
-        for (int it = 0; it < 64 / RPI; ++it) {
-            const int r = it * RPI + rl;
-            const int64_t grow = row0 + half * 64 + r;
+        for (int it = 0; it < 16 / GPI; ++it) {
+            const int g = it * GPI + gl;  // row group: rows 4g .. 4g+3 of this half
+            const uint8_t *src = reg + g * RGS + epi_col_offset<W>(cl * 8);
+            uint4 q[4];  // q[k]: columns 8cl + 2k, 2k+1; .x/.y rows 0-1/2-3 of the first, .z/.w of the second
+#pragma unroll
+            for (int k = 0; k < 4; ++k) q[k] = *reinterpret_cast<const uint4 *>(src + k * 16);
+            uint4 rowv[4];
+            {
+                uint32_t w[4][4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    w[0][k] = __builtin_amdgcn_perm(q[k].z, q[k].x, 0x05040100u);  // row 0: low halves
+                    w[1][k] = __builtin_amdgcn_perm(q[k].z, q[k].x, 0x07060302u);  // row 1: high halves
+                    w[2][k] = __builtin_amdgcn_perm(q[k].w, q[k].y, 0x05040100u);
+                    w[3][k] = __builtin_amdgcn_perm(q[k].w, q[k].y, 0x07060302u);
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) rowv[r] = make_uint4(w[r][0], w[r][1], w[r][2], w[r][3]);
+            }
             const int64_t col = col0 + cl * 8;
-            const uint4 v = *reinterpret_cast<const uint4 *>(reg + r * RS + cl * 16);
-            if constexpr (EPI == QIM_EPI_SWIGLU_QUANT) {
-                float f[8];
-                unpack8(v, f);
-                const uint32_t m = group_umax<4>(absmax_bits8(f));
-                const int e = mx_exponent(__uint_as_float(m));
-                const float inv = mx_inverse(e);
-                uint2 c;
-                c.x = cvt_e4m3x4(f[0] * inv, f[1] * inv, f[2] * inv, f[3] * inv);
-                c.y = cvt_e4m3x4(f[4] * inv, f[5] * inv, f[6] * inv, f[7] * inv);
-                if (grow < p.Mp) {
-                    *reinterpret_cast<uint2 *>(reinterpret_cast<uint8_t *>(p.out) + grow * F + col) = c;
-                    if ((cl & 3) == 0) p.out_scales[mx_scale_offset(grow, col >> 5, F)] = (uint8_t)e;
-                }
-            } else {
-                if (grow >= p.M) continue;
-                uint4 o = v;
-                if constexpr (EPI == QIM_EPI_GATED_RESIDUAL) {
-                    const uint4 hv = *reinterpret_cast<const uint4 *>(p.res + grow * p.N + col);
-                    const uint4 gv = *reinterpret_cast<const uint4 *>(p.gate + (grow / p.seq) * p.N + col);
-                    float y[8], h[8], g[8], z[8];
-                    unpack8(v, y);
-                    unpack8(hv, h);
-                    unpack8(gv, g);
 #pragma unroll
-                    for (int t = 0; t < 8; ++t) z[t] = h[t] + rbf(g[t] * y[t]);
-                    o = pack8(z);
+            for (int r = 0; r < 4; ++r) {
+                const int64_t grow = row0 + half * 64 + 4 * g + r;
+                const uint4 v = rowv[r];
+                if constexpr (EPI == QIM_EPI_SWIGLU_QUANT) {
+                    float f[8];
+                    unpack8(v, f);
+                    const uint32_t m = group_umax<4>(absmax_bits8(f));
+                    const int e = mx_exponent(__uint_as_float(m));
+                    const float inv = mx_inverse(e);
+                    uint2 c;
+                    c.x = cvt_e4m3x4(f[0] * inv, f[1] * inv, f[2] * inv, f[3] * inv);
+                    c.y = cvt_e4m3x4(f[4] * inv, f[5] * inv, f[6] * inv, f[7] * inv);
+                    if (grow < p.Mp) {
+                        *reinterpret_cast<uint2 *>(reinterpret_cast<uint8_t *>(p.out) + grow * F + col) = c;
+                        if ((cl & 3) == 0) p.out_scales[mx_scale_offset(grow, col >> 5, F)] = (uint8_t)e;
+                    }
+                } else {
+                    if (grow >= p.M) continue;
+                    uint4 o = v;
+                    if constexpr (EPI == QIM_EPI_GATED_RESIDUAL) {
+                        const uint4 hv = *reinterpret_cast<const uint4 *>(p.res + grow * p.N + col);
+                        const uint4 gv = *reinterpret_cast<const uint4 *>(p.gate + (grow / p.seq) * p.N + col);
+                        float y[8], h[8], gg[8], z[8];
+                        unpack8(v, y);
+                        unpack8(hv, h);
+                        unpack8(gv, gg);
+#pragma unroll
+                        for (int t = 0; t < 8; ++t) z[t] = h[t] + rbf(gg[t] * y[t]);
+                        o = pack8(z);
+                    }
+                    *reinterpret_cast<uint4 *>(reinterpret_cast<uint16_t *>(p.out) + grow * p.ldo + col) = o;
                 }
-                *reinterpret_cast<uint4 *>(reinterpret_cast<uint16_t *>(p.out) + grow * p.ldo + col) = o;
             }
         }
     }
 }
-
 
 // ------------------------------------------------------------ tail tiles --
 // The tile grid is rarely a whole number of rounds of the CUs (4352 x 12288:
