@@ -213,30 +213,34 @@ def bench_quantize(steps, warmup):
                 frac=nbytes / us / 1e3 / HBM_PEAK_GBS, shape="[4352,3072]")
 
 
-def bench_gemm(steps, warmup):
-    """Config 4b: MXFP8 GEMM [4352 x 3072] x [3072 x 12288] + bias."""
+def bench_gemm(steps, warmup, tiled=True):
+    """Config 4b: MXFP8 GEMM [4352 x 3072] x [3072 x 12288] + bias.  ``tiled``:
+    both operands in the tiled code layout MXFP8Linear uses (weight quantized
+    once, activation quantized with tiled=True); else the reference's
+    row-major codes."""
     from qwen_image_accel import _native
     from qwen_image_accel.kernels import mxfp8
     g = gen(1)
     M, K, N = 4352, 3072, 12288
     a = torch.randn(M, K, generator=g)
     a[torch.rand(M, K, generator=g) < 0.01] *= 20
-    aq = mxfp8.quantize(a.to(torch.bfloat16).cuda())
-    wq = mxfp8.quantize(randn(g, (N, K), 0.02))
+    aq = mxfp8.quantize(a.to(torch.bfloat16).cuda(), tiled=tiled)
+    wq = mxfp8.quantize(randn(g, (N, K), 0.02), tiled=tiled)
     bias = randn(g, (N,), 0.01)
     out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
     flops = 2 * M * N * K
     L = _native.lib()
+    layouts = _native.GEMM_A_TILED | _native.GEMM_B_TILED if tiled else 0
 
     def step(i):
-        rc = L.qim_mxfp8_gemm(aq.values.data_ptr(), aq.scales.data_ptr(), wq.values.data_ptr(),
-                              wq.scales.data_ptr(), M, N, K, _native.EPI_BIAS, bias.data_ptr(), None, None,
-                              M, out.data_ptr(), N, None, torch.cuda.current_stream().cuda_stream)
+        rc = L.qim_mxfp8_gemm_ex(aq.values.data_ptr(), aq.scales.data_ptr(), wq.values.data_ptr(),
+                                 wq.scales.data_ptr(), M, N, K, _native.EPI_BIAS, layouts, bias.data_ptr(), None,
+                                 None, M, out.data_ptr(), N, None, torch.cuda.current_stream().cuda_stream)
         assert rc == 0
     us = Timed(step, max(10, steps // 4), warmup).run() * 1e3
     tf = flops / us / 1e6
     return dict(kernel="qim_mxfp8_gemm", us=us, flops=flops, tflops=tf, frac=tf / MXFP8_PEAK_TFLOPS,
-                shape="4352x3072x12288 +bias")
+                shape="4352x3072x12288 +bias", layout="tiled" if tiled else "row-major")
 
 
 def bench_block(tokens, steps, warmup):
@@ -346,6 +350,7 @@ def main():
                      ("gated_residual_1024", lambda: bench_residual(steps, warm)),
                      ("quantize_1024", lambda: bench_quantize(steps, warm)),
                      ("mxfp8_gemm_bias_1024", lambda: bench_gemm(steps, warm)),
+                     ("mxfp8_gemm_bias_1024_rowmajor", lambda: bench_gemm(steps, warm, tiled=False)),
                      ("block_1024", lambda: bench_block(4352, steps, warm)),
                      ("block_2048", lambda: bench_block(16640, steps, warm)),
                      ("copy_256MiB", lambda: bench_copy(steps, warm))]:

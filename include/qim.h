@@ -35,6 +35,7 @@ enum qim_status {
 
 /* Flags of qim_adaln / qim_adaln_quantize. */
 #define QIM_ADALN_ADD_ONE 1 /* use bf16(1 + scale) instead of scale */
+#define QIM_ADALN_TILED 2   /* qim_adaln_quantize: codes in the tiled layout (below) */
 
 /* Epilogues of qim_mxfp8_gemm. */
 enum qim_epilogue {
@@ -62,6 +63,11 @@ int qim_abi_version(void);
 int qim_mx_quantize(const void *x, int64_t ldx, int64_t M, int64_t K,
                     void *q, void *scales, void *stream);
 
+/* qim_mx_quantize writing the codes in the tiled layout (QIM_GEMM_A_TILED /
+ * QIM_GEMM_B_TILED operands of qim_mxfp8_gemm_ex).  No reference counterpart. */
+int qim_mx_quantize_tiled(const void *x, int64_t ldx, int64_t M, int64_t K,
+                          void *q, void *scales, void *stream);
+
 /* layer_norm_scale(x, scale, norm) -- src/qwen_image_accel/kernels/
  * layernorm.py:58-86 (kernel :17-55), extended with the optional MMDiT shift,
  * gate and residual: out = res + gate * (scale * LN(x) + shift) with a bf16
@@ -74,7 +80,8 @@ int qim_adaln(const void *x, const void *scale, const void *shift, const void *g
 
 /* layer_norm_scale_quantize(x, scale, norm) -- src/qwen_image_accel/kernels/
  * epilogue.py:145-161 (kernel :92-142): qim_adaln's output quantized to MXFP8
- * instead of stored.  q: (Mp, D); scales: Mp*D/32.  D % 128 == 0. */
+ * instead of stored.  q: (Mp, D), row-major or (QIM_ADALN_TILED) tiled;
+ * scales: Mp*D/32.  D % 128 == 0. */
 int qim_adaln_quantize(const void *x, const void *scale, const void *shift, const void *gate,
                        const void *res, void *q, void *scales, int64_t rows, int64_t D,
                        int64_t seq, float eps, int flags, void *stream);
@@ -97,6 +104,11 @@ int qim_swiglu(const void *g, int64_t ldg, const void *v, int64_t ldv, void *out
  * scales: Mp*F/32.  F % 128 == 0. */
 int qim_swiglu_quantize(const void *g, int64_t ldg, const void *v, int64_t ldv,
                         void *q, void *scales, int64_t M, int64_t F, void *stream);
+
+/* qim_swiglu_quantize writing the codes in the tiled layout.  No reference
+ * counterpart. */
+int qim_swiglu_quantize_tiled(const void *g, int64_t ldg, const void *v, int64_t ldv,
+                              void *q, void *scales, int64_t M, int64_t F, void *stream);
 
 /* rms_norm(x, weight, eps) -- src/qwen_image_accel/kernels/bf16.py:58-63
  * (kernel :46-55): out = bf16(bf16(x * rsqrt(mean(x^2) + eps)) * w) per row of
@@ -139,6 +151,26 @@ int qim_mxfp8_gemm(const void *aq, const void *as, const void *bq, const void *b
                    int64_t M, int64_t N, int64_t K, int epilogue, const void *bias,
                    const void *gate, const void *res, int64_t seq, void *out, int64_t ldo,
                    void *out_scales, void *stream);
+
+/* Tiled E4M3 code layout (no reference counterpart: the reference hands
+ * row-major codes to torch._scaled_mm).  An (R, K) code matrix, R % 128 == 0,
+ * is stored in super-blocks of 256 rows (the last holds R % 256 rows when that
+ * is 128).  In a super-block of n rows starting at row r0, the 64-byte K-slab
+ * s (codes [64s, 64s + 64) of each row) is n*64 contiguous bytes at
+ * r0*K + s*n*64; row r's 64 bytes sit at (r - r0)*64 inside it, with its
+ * 16-byte chunk c at chunk position c ^ (((r >> 1) ^ (r >> 2)) & 3).  Every
+ * 16-row group of a slab is then the 1 KiB LDS image the GEMM loads with one
+ * contiguous DMA instruction.  Scales keep the swizzled layout above. */
+#define QIM_GEMM_A_TILED 1   /* aq is tiled over Mp rows                          */
+#define QIM_GEMM_B_TILED 2   /* bq is tiled over N rows                           */
+#define QIM_GEMM_OUT_TILED 4 /* QIM_EPI_SWIGLU_QUANT codes are written tiled      */
+
+/* qim_mxfp8_gemm with operand layouts (an OR of the flags above; 0 = both
+ * row-major, which is qim_mxfp8_gemm itself). */
+int qim_mxfp8_gemm_ex(const void *aq, const void *as, const void *bq, const void *bs,
+                      int64_t M, int64_t N, int64_t K, int epilogue, int layouts,
+                      const void *bias, const void *gate, const void *res, int64_t seq,
+                      void *out, int64_t ldo, void *out_scales, void *stream);
 
 /* Test hooks: the device conversions every kernel uses, applied elementwise
  * (fp32 -> E4M3 code; fp32 -> bf16 bits), and one scaled MFMA

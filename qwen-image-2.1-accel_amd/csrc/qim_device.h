@@ -99,6 +99,24 @@ __device__ __forceinline__ int64_t mx_scale_offset(int64_t r, int64_t kb, int64_
     return ((r >> 7) * (K >> 7) + (kb >> 2)) * 512 + (r & 31) * 16 + ((r & 127) >> 5) * 4 + (kb & 3);
 }
 
+// Position of 16-byte chunk c (0..3) of row r's 64-byte K-slab in LDS and in
+// the tiled code layout: chunk c ^ swizzle(r), which spreads the rows read by
+// one ds_read_b128 group over distinct banks.
+__device__ __forceinline__ int mx_chunk_swizzle(int64_t r) { return (int)(((r >> 1) ^ (r >> 2)) & 3); }
+
+// Byte offset of code (r, k) of an (R, K) E4M3 matrix (R % 128 == 0) in the
+// tiled layout: rows in super-blocks of 256 (the last holds R % 256 rows if
+// that is 128); inside a super-block of n rows from row r0, 64-byte K-slab s
+// is n * 64 contiguous bytes at r0 * K + s * n * 64, row r's 64 bytes at
+// (r - r0) * 64 inside it, and its 16-byte chunk c at chunk c ^ swizzle(r).
+// One 16-row group of one slab is then exactly the 1 KiB LDS image the GEMM
+// loads with one contiguous DMA instruction.
+__device__ __forceinline__ int64_t mxt_offset(int64_t r, int64_t k, int64_t R, int64_t K) {
+    const int64_t r0 = r & ~int64_t(255);
+    const int64_t n = R - r0 < 256 ? R - r0 : 256;
+    return r0 * K + (k >> 6) * n * 64 + (r - r0) * 64 + ((((k >> 4) & 3) ^ mx_chunk_swizzle(r)) << 4) + (k & 15);
+}
+
 // |x| maximum of 8 values, as an fp32 bit pattern compared as unsigned
 // (monotonic for non-NaN values; no canonicalisation needed).
 __device__ __forceinline__ uint32_t absmax_bits8(const float *f) {

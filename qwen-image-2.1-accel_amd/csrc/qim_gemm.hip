@@ -51,9 +51,10 @@ struct GemmArgs {
     uint8_t *out_scales;
     int tiles_m, tiles_n;
     int main_tiles;  // whole tiles; workgroups past them compute quarter tiles of the rest
+    int a_tiled, b_tiled, out_tiled;  // code layouts (mxt_offset) of A, B and a quantized output
 };
 
-__device__ __forceinline__ int kswz(int row) { return ((row >> 1) ^ (row >> 2)) & 3; }
+__device__ __forceinline__ int kswz(int row) { return mx_chunk_swizzle(row); }
 // LDS byte offset of logical 16-byte chunk c of tile row `row` (64-byte rows).
 __device__ __forceinline__ int lds_off(int row, int c) { return row * BK + ((c ^ kswz(row)) << 4); }
 
@@ -64,12 +65,38 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 __device__ __forceinline__ void block_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
+// Stage-0 source offset of this lane's 16 bytes in the DMA of the 16 tile
+// rows [grp, grp + 16) of an (R, K) code matrix whose tile starts at row m0:
+// lane i lands at row grp + i/4, physical LDS chunk i%4.  Row-major codes:
+// the lane's logical chunk of its row.  Tiled codes (mxt_offset): the group is
+// already the LDS image, 1 KiB contiguous.  Rows past R are clamped into the
+// matrix; they only feed output rows that are never stored.
+__device__ __forceinline__ uint32_t opnd_offset(int64_t m0, int grp, int lane, int64_t R, int64_t K, bool tiled) {
+    if (!tiled) {
+        const int row = grp + (lane >> 2);
+        int64_t r = m0 + row;
+        r = r < R ? r : R - 1;
+        return (uint32_t)(r * K + (((lane & 3) ^ kswz(row)) << 4));
+    }
+    int64_t rg = m0 + grp;
+    rg = rg <= R - 16 ? rg : R - 16;
+    const int64_t r0 = rg & ~int64_t(255);
+    return (uint32_t)(r0 * K + (rg - r0) * 64 + lane * 16);
+}
+// Advance of those offsets per 64-byte K stage (wave-uniform).
+__device__ __forceinline__ uint32_t opnd_step(int64_t m0, int64_t R, bool tiled) {
+    if (!tiled) return BK;
+    const int64_t r0 = m0 & ~int64_t(255);
+    return (uint32_t)((R - r0 < 256 ? R - r0 : 256) * 64);
+}
+
 // Per-lane source offsets of the 10 load instructions of a stage (stage 0);
-// stage s adds s * 64 (operands) or (s / 2) * 512 (scales).
+// stage s adds s * astep / s * bstep (operands) or (s / 2) * 512 (scales).
 struct LoadPlan {
     uint32_t a[4], b[4];      // byte offsets into aq / bq
     uint32_t sc[2];           // byte offsets into sc_base
     const uint8_t *sc_base[2];  // as (A scale quarter) or bs (B scale quarter); wave-uniform
+    uint32_t astep, bstep;
     int wave;
 };
 
@@ -79,13 +106,12 @@ __device__ __forceinline__ LoadPlan make_plan(const GemmArgs &p, int64_t m0, int
     L.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int row = (L.wave * 4 + j) * 16 + (lane >> 2);
-        const int c = (lane & 3) ^ kswz(row);
-        int64_t ar = m0 + row;
-        ar = ar < p.Mp ? ar : p.Mp - 1;  // rows past Mp only feed output rows that are never stored
-        L.a[j] = (uint32_t)(ar * p.K + c * 16);
-        L.b[j] = (uint32_t)((n0 + row) * p.K + c * 16);
+        const int grp = (L.wave * 4 + j) * 16;
+        L.a[j] = opnd_offset(m0, grp, lane, p.Mp, p.K, p.a_tiled);
+        L.b[j] = opnd_offset(n0, grp, lane, p.N, p.K, p.b_tiled);
     }
+    L.astep = opnd_step(m0, p.Mp, p.a_tiled);
+    L.bstep = opnd_step(n0, p.N, p.b_tiled);
     const int64_t kt = p.K / 128;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -126,12 +152,12 @@ __device__ __forceinline__ uint32_t lds_addr(const uint8_t *p) {
 }
 
 __device__ __forceinline__ void issue_stage(const GemmArgs &p, const LoadPlan &L, uint8_t *slot, int s) {
-    const uint32_t kofs = (uint32_t)s * BK;
+    const uint32_t ka = (uint32_t)s * L.astep, kb = (uint32_t)s * L.bstep;
     const uint32_t base = lds_addr(slot);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) dma16(p.aq, L.a[j] + kofs, base + (L.wave * 4 + j) * 1024);
+    for (int j = 0; j < 4; ++j) dma16(p.aq, L.a[j] + ka, base + (L.wave * 4 + j) * 1024);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) dma16(p.bq, L.b[j] + kofs, base + TILE_BYTES + (L.wave * 4 + j) * 1024);
+    for (int j = 0; j < 4; ++j) dma16(p.bq, L.b[j] + kb, base + TILE_BYTES + (L.wave * 4 + j) * 1024);
     const uint32_t gofs = (uint32_t)(s >> 1) * 512;
 #pragma unroll
     for (int j = 0; j < 2; ++j)
@@ -203,7 +229,7 @@ __device__ __forceinline__ void pipeline_step(const GemmArgs &p, const LoadPlan 
     uint8_t *fill = lds + (s & 3) * STAGE_BYTES;
     const uint8_t *next = lds + ((s + 1) & 3) * STAGE_BYTES;  // stale at the last stage; unused then
     const int sl = s + 4 < S ? s + 4 : S - 1;                 // stage to load (clamped)
-    const uint32_t kofs = (uint32_t)sl * BK, gofs = (uint32_t)(sl >> 1) * 512;
+    const uint32_t ka = (uint32_t)sl * L.astep, kb = (uint32_t)sl * L.bstep, gofs = (uint32_t)(sl >> 1) * 512;
     const uint32_t fb = lds_addr(fill);
     const int ra0 = wm * 128 + lr, rb0 = wn * 128 + lr;
 
@@ -216,21 +242,21 @@ __device__ __forceinline__ void pipeline_step(const GemmArgs &p, const LoadPlan 
     wait_vmcnt<2 * LOADS_PER_STAGE>();
     block_barrier();
     QIM_SCHED();
-    QIM_STEP(0, 1, dma16(p.aq, L.a[0] + kofs, fb + (w4 + 0) * 1024));
+    QIM_STEP(0, 1, dma16(p.aq, L.a[0] + ka, fb + (w4 + 0) * 1024));
     // The next stage's scales: the same 128-K group after an even stage (kept
     // in registers), a new group after an odd one (one 16-byte read each).
-    QIM_STEP(0, 2, dma16(p.aq, L.a[1] + kofs, fb + (w4 + 1) * 1024);
+    QIM_STEP(0, 2, dma16(p.aq, L.a[1] + ka, fb + (w4 + 1) * 1024);
              if constexpr (PAR == 0) nxt.sa = cur.sa; else nxt.sa = read_scales(nsa, wm, lr));
-    QIM_STEP(0, 3, dma16(p.aq, L.a[2] + kofs, fb + (w4 + 2) * 1024);
+    QIM_STEP(0, 3, dma16(p.aq, L.a[2] + ka, fb + (w4 + 2) * 1024);
              if constexpr (PAR == 0) nxt.sb = cur.sb; else nxt.sb = read_scales(nsb, wn, lr));
-    QIM_STEP(1, 0, dma16(p.aq, L.a[3] + kofs, fb + (w4 + 3) * 1024); nxt.a[0] = read_tile(next, ra0, kh));
-    QIM_STEP(1, 1, dma16(p.bq, L.b[0] + kofs, fb + TILE_BYTES + (w4 + 0) * 1024);
+    QIM_STEP(1, 0, dma16(p.aq, L.a[3] + ka, fb + (w4 + 3) * 1024); nxt.a[0] = read_tile(next, ra0, kh));
+    QIM_STEP(1, 1, dma16(p.bq, L.b[0] + kb, fb + TILE_BYTES + (w4 + 0) * 1024);
              nxt.b[0] = read_tile(next + TILE_BYTES, rb0, kh));
-    QIM_STEP(1, 2, dma16(p.bq, L.b[1] + kofs, fb + TILE_BYTES + (w4 + 1) * 1024);
+    QIM_STEP(1, 2, dma16(p.bq, L.b[1] + kb, fb + TILE_BYTES + (w4 + 1) * 1024);
              nxt.b[1] = read_tile(next + TILE_BYTES, rb0 + 32, kh));
-    QIM_STEP(1, 3, dma16(p.bq, L.b[2] + kofs, fb + TILE_BYTES + (w4 + 2) * 1024);
+    QIM_STEP(1, 3, dma16(p.bq, L.b[2] + kb, fb + TILE_BYTES + (w4 + 2) * 1024);
              nxt.b[2] = read_tile(next + TILE_BYTES, rb0 + 64, kh));
-    QIM_STEP(2, 0, dma16(p.bq, L.b[3] + kofs, fb + TILE_BYTES + (w4 + 3) * 1024);
+    QIM_STEP(2, 0, dma16(p.bq, L.b[3] + kb, fb + TILE_BYTES + (w4 + 3) * 1024);
              nxt.b[3] = read_tile(next + TILE_BYTES, rb0 + 96, kh));
     QIM_STEP(2, 1, dma4(scb0, L.sc[0] + gofs, fb + 2 * TILE_BYTES + (L.wave * 2 + 0) * 256);
              nxt.a[1] = read_tile(next, ra0 + 32, kh));
@@ -381,7 +407,8 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
                     c.x = cvt_e4m3x4(f[0] * inv, f[1] * inv, f[2] * inv, f[3] * inv);
                     c.y = cvt_e4m3x4(f[4] * inv, f[5] * inv, f[6] * inv, f[7] * inv);
                     if (grow < p.Mp) {
-                        *reinterpret_cast<uint2 *>(reinterpret_cast<uint8_t *>(p.out) + grow * F + col) = c;
+                        const int64_t o = p.out_tiled ? mxt_offset(grow, col, p.Mp, F) : grow * F + col;
+                        *reinterpret_cast<uint2 *>(reinterpret_cast<uint8_t *>(p.out) + o) = c;
                         if ((cl & 3) == 0) p.out_scales[mx_scale_offset(grow, col >> 5, F)] = (uint8_t)e;
                     }
                 } else {
@@ -419,6 +446,7 @@ struct QPlan {
     uint32_t a[2], b[2];   // byte offsets into aq / bq (stage 0)
     uint32_t sc;           // byte offset of this wave's 256 scale bytes (stage 0)
     const uint8_t *sc_base;
+    uint32_t astep, bstep;
     int wave;
 };
 
@@ -428,13 +456,12 @@ __device__ __forceinline__ QPlan make_qplan(const GemmArgs &p, int64_t m0, int64
     Q.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-        const int row = (Q.wave * 2 + j) * 16 + (lane >> 2);
-        const int c = (lane & 3) ^ kswz(row);
-        int64_t ar = m0 + row;
-        ar = ar < p.Mp ? ar : p.Mp - 1;
-        Q.a[j] = (uint32_t)(ar * p.K + c * 16);
-        Q.b[j] = (uint32_t)((n0 + row) * p.K + c * 16);
+        const int grp = (Q.wave * 2 + j) * 16;
+        Q.a[j] = opnd_offset(m0, grp, lane, p.Mp, p.K, p.a_tiled);
+        Q.b[j] = opnd_offset(n0, grp, lane, p.N, p.K, p.b_tiled);
     }
+    Q.astep = opnd_step(m0, p.Mp, p.a_tiled);
+    Q.bstep = opnd_step(n0, p.N, p.b_tiled);
     // Waves 0, 1 load the A scale chunk of rows [m0, m0 + 128), waves 2, 3 the B chunk.
     const int64_t kt = p.K / 128;
     const int64_t grow = Q.wave < 2 ? m0 / 128 : n0 / 128;
@@ -444,11 +471,11 @@ __device__ __forceinline__ QPlan make_qplan(const GemmArgs &p, int64_t m0, int64
 }
 
 __device__ __forceinline__ void issue_qstage(const GemmArgs &p, const QPlan &Q, uint8_t *slot, int s) {
-    const uint32_t kofs = (uint32_t)s * BK, base = lds_addr(slot), w2 = Q.wave * 2;
-    dma16(p.aq, Q.a[0] + kofs, base + (w2 + 0) * 1024);
-    dma16(p.aq, Q.a[1] + kofs, base + (w2 + 1) * 1024);
-    dma16(p.bq, Q.b[0] + kofs, base + TILE_BYTES + (w2 + 0) * 1024);
-    dma16(p.bq, Q.b[1] + kofs, base + TILE_BYTES + (w2 + 1) * 1024);
+    const uint32_t ka = (uint32_t)s * Q.astep, kb = (uint32_t)s * Q.bstep, base = lds_addr(slot), w2 = Q.wave * 2;
+    dma16(p.aq, Q.a[0] + ka, base + (w2 + 0) * 1024);
+    dma16(p.aq, Q.a[1] + ka, base + (w2 + 1) * 1024);
+    dma16(p.bq, Q.b[0] + kb, base + TILE_BYTES + (w2 + 0) * 1024);
+    dma16(p.bq, Q.b[1] + kb, base + TILE_BYTES + (w2 + 1) * 1024);
     dma4(Q.sc_base, Q.sc + (uint32_t)(s >> 1) * 512,
          base + 2 * TILE_BYTES + (Q.wave < 2 ? 0 : SCALE_BYTES) + (Q.wave & 1) * 256);
 }
@@ -622,10 +649,15 @@ static int launch_gemm(const GemmArgs &a, int64_t tiles, hipStream_t st) {
 
 using namespace qim;
 
-extern "C" int qim_mxfp8_gemm(const void *aq, const void *as, const void *bq, const void *bs, int64_t M, int64_t N,
-                              int64_t K, int epilogue, const void *bias, const void *gate, const void *res,
-                              int64_t seq, void *out, int64_t ldo, void *out_scales, void *stream) {
+extern "C" int qim_mxfp8_gemm_ex(const void *aq, const void *as, const void *bq, const void *bs, int64_t M,
+                                 int64_t N, int64_t K, int epilogue, int layouts, const void *bias, const void *gate,
+                                 const void *res, int64_t seq, void *out, int64_t ldo, void *out_scales,
+                                 void *stream) {
     QIM_REQUIRE(aq && as && bq && bs && out, QIM_ERR_ARG, "qim_mxfp8_gemm: null pointer");
+    QIM_REQUIRE((layouts & ~(QIM_GEMM_A_TILED | QIM_GEMM_B_TILED | QIM_GEMM_OUT_TILED)) == 0, QIM_ERR_ARG,
+                "qim_mxfp8_gemm: unknown layout flags 0x%x", layouts);
+    QIM_REQUIRE(!(layouts & QIM_GEMM_OUT_TILED) || epilogue == QIM_EPI_SWIGLU_QUANT, QIM_ERR_ARG,
+                "qim_mxfp8_gemm: a tiled output needs the quantized SwiGLU epilogue");
     QIM_REQUIRE(M > 0 && N > 0 && K > 0, QIM_ERR_SHAPE, "qim_mxfp8_gemm: empty problem");
     QIM_REQUIRE(K % 128 == 0, QIM_ERR_SHAPE, "qim_mxfp8_gemm: K=%lld is not a multiple of 128", (long long)K);
     QIM_REQUIRE(N % BN == 0, QIM_ERR_SHAPE, "qim_mxfp8_gemm: N=%lld is not a multiple of 256", (long long)N);
@@ -641,7 +673,9 @@ extern "C" int qim_mxfp8_gemm(const void *aq, const void *as, const void *bq, co
                 "qim_mxfp8_gemm: operands above 2 GiB are not supported");
     GemmArgs a{(const uint8_t *)aq, (const uint8_t *)as, (const uint8_t *)bq, (const uint8_t *)bs, M, Mp, N, K,
                (const uint16_t *)bias, (const uint16_t *)gate, (const uint16_t *)res, seq > 0 ? seq : M, out, ldo,
-               (uint8_t *)out_scales, (int)tiles_m, (int)tiles_n, 0};
+               (uint8_t *)out_scales, (int)tiles_m, (int)tiles_n, 0,
+               (layouts & QIM_GEMM_A_TILED) != 0, (layouts & QIM_GEMM_B_TILED) != 0,
+               (layouts & QIM_GEMM_OUT_TILED) != 0};
     const int64_t tiles = tiles_m * tiles_n;
     a.main_tiles = (int)main_tile_count(tiles);
     int rc;
@@ -674,4 +708,11 @@ extern "C" int qim_mxfp8_gemm(const void *aq, const void *as, const void *bq, co
             return fail(QIM_ERR_ARG, "qim_mxfp8_gemm: unknown epilogue %d", epilogue);
     }
     return rc ? rc : check_launch("qim_mxfp8_gemm");
+}
+
+extern "C" int qim_mxfp8_gemm(const void *aq, const void *as, const void *bq, const void *bs, int64_t M, int64_t N,
+                              int64_t K, int epilogue, const void *bias, const void *gate, const void *res,
+                              int64_t seq, void *out, int64_t ldo, void *out_scales, void *stream) {
+    return qim_mxfp8_gemm_ex(aq, as, bq, bs, M, N, K, epilogue, 0, bias, gate, res, seq, out, ldo, out_scales,
+                             stream);
 }

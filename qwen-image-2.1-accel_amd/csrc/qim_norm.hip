@@ -26,7 +26,13 @@ struct AdaLNArgs {
     int64_t seq;
     float eps;
     int flags;
+    int tiled;         // quantized codes in the GEMM's tiled layout (mxt_offset over rows_pad rows)
 };
+
+// Byte offset of codes [8j, 8j + 8) of a quantized row.
+__device__ __forceinline__ int64_t adaln_code_offset(const AdaLNArgs &p, int64_t row, int j) {
+    return p.tiled ? mxt_offset(row, (int64_t)j * 8, p.rows_pad, p.D) : row * p.D + (int64_t)j * 8;
+}
 
 constexpr int ADALN_MAX_WAVES = 16;    // 1024 threads per row (masked kernel)
 constexpr int ADALN_FULL_WAVES = 4;    // full-coverage kernels: 256 threads, no register cap below 512
@@ -61,7 +67,7 @@ __global__ __launch_bounds__(FULL ? 64 * ADALN_FULL_WAVES : 64 * ADALN_MAX_WAVES
             for (int i = 0; i < NV; ++i) {
                 const int j = tid + nthr * i;
                 if (!FULL && j >= nvec) break;
-                st_nt(reinterpret_cast<uint2 *>(p.q + row * p.D) + j, make_uint2(0, 0));
+                st_nt(p.q + adaln_code_offset(p, row, j), make_uint2(0, 0));
                 if ((lane & 15) == 0)
                     *reinterpret_cast<uint32_t *>(p.qs + mx_scale_offset(row, j >> 2, p.D)) = 0u;
             }
@@ -197,7 +203,7 @@ __global__ __launch_bounds__(FULL ? 64 * ADALN_FULL_WAVES : 64 * ADALN_MAX_WAVES
             uint2 c;
             c.x = cvt_e4m3x4(o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv);
             c.y = cvt_e4m3x4(o[4] * inv, o[5] * inv, o[6] * inv, o[7] * inv);
-            st_nt(reinterpret_cast<uint2 *>(p.q + row * p.D) + j, c);
+            st_nt(p.q + adaln_code_offset(p, row, j), c);
             const uint32_t e1 = (uint32_t)__shfl((int)e, lane + 4, 64);
             const uint32_t e2 = (uint32_t)__shfl((int)e, lane + 8, 64);
             const uint32_t e3 = (uint32_t)__shfl((int)e, lane + 12, 64);
@@ -450,7 +456,7 @@ extern "C" int qim_adaln(const void *x, const void *scale, const void *shift, co
     if (rc) return rc;
     QIM_REQUIRE(out && aligned16(out), QIM_ERR_LAYOUT, "qim_adaln: out must be a 16-byte aligned pointer");
     AdaLNArgs a{(const uint16_t *)x, (const uint16_t *)scale, (const uint16_t *)shift, (const uint16_t *)gate,
-                (const uint16_t *)res, (uint16_t *)out, nullptr, nullptr, rows, rows, (int)D, seq, eps, flags};
+                (const uint16_t *)res, (uint16_t *)out, nullptr, nullptr, rows, rows, (int)D, seq, eps, flags, 0};
     rc = launch_adaln<false>(a, as_stream(stream));
     return rc ? rc : check_launch("qim_adaln");
 }
@@ -465,7 +471,7 @@ extern "C" int qim_adaln_quantize(const void *x, const void *scale, const void *
                 "qim_adaln_quantize: q and scales must be 16-byte aligned pointers");
     AdaLNArgs a{(const uint16_t *)x, (const uint16_t *)scale, (const uint16_t *)shift, (const uint16_t *)gate,
                 (const uint16_t *)res, nullptr, (uint8_t *)q, (uint8_t *)scales, rows, (rows + 127) / 128 * 128,
-                (int)D, seq, eps, flags};
+                (int)D, seq, eps, flags, (flags & QIM_ADALN_TILED) != 0};
     rc = launch_adaln<true>(a, as_stream(stream));
     return rc ? rc : check_launch("qim_adaln_quantize");
 }

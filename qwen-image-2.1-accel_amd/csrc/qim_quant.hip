@@ -8,7 +8,8 @@
 // 8 passes.  A 32-element block is 4 adjacent lanes, reduced with two DPP
 // quad permutes.  All 8 loads of a lane are issued before any arithmetic.
 // HBM traffic is the algorithmic minimum: every input byte read once, every
-// code and scale byte written once.
+// code and scale byte written once.  Codes are written row-major or in the
+// GEMM's tiled layout (mxt_offset); an 8-byte store stays contiguous in both.
 #include "qim_device.h"
 #include "qim_runtime.h"
 
@@ -65,7 +66,7 @@ __device__ __forceinline__ uint2 quantize8(const float *f, int &e) {
 template <class Source>
 __global__ __launch_bounds__(256) void k_quant_tile(Source src, uint8_t *__restrict__ q,
                                                      uint8_t *__restrict__ scales, int64_t M,
-                                                     int64_t K) {
+                                                     int64_t K, int tiled) {
     __shared__ uint4 s_scale[32];  // the tile's 512 swizzled exponent bytes
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int c16 = lane & 15;    // 8-column chunk of the 128-column tile row
@@ -87,7 +88,8 @@ __global__ __launch_bounds__(256) void k_quant_tile(Source src, uint8_t *__restr
         src.values(a[i], b[i], f);
         int e;
         uint2 c = quantize8(f, e);
-        st_nt(q + (row0 + r) * K + col, c);
+        const int64_t Mp = (int64_t)gridDim.x * 128;
+        st_nt(q + (tiled ? mxt_offset(row0 + r, col, Mp, K) : (row0 + r) * K + col), c);
         if ((c16 & 3) == 0) sb[(r & 31) * 16 + wave * 4 + (c16 >> 2)] = (uint8_t)e;
     }
     __syncthreads();
@@ -108,8 +110,8 @@ static int launch_quant_checks(const char *what, int64_t M, int64_t K) {
 
 using namespace qim;
 
-extern "C" int qim_mx_quantize(const void *x, int64_t ldx, int64_t M, int64_t K, void *q, void *scales,
-                               void *stream) {
+static int mx_quantize(const void *x, int64_t ldx, int64_t M, int64_t K, void *q, void *scales, int tiled,
+                       void *stream) {
     QIM_REQUIRE(x && q && scales, QIM_ERR_ARG, "qim_mx_quantize: null pointer");
     int rc = launch_quant_checks("qim_mx_quantize", M, K);
     if (rc) return rc;
@@ -118,12 +120,12 @@ extern "C" int qim_mx_quantize(const void *x, int64_t ldx, int64_t M, int64_t K,
     dim3 grid((unsigned)((M + 127) / 128), (unsigned)(K / 128));
     QuantSource src{(const uint16_t *)x, ldx};
     hipLaunchKernelGGL(k_quant_tile<QuantSource>, grid, dim3(256), 0, as_stream(stream), src, (uint8_t *)q,
-                       (uint8_t *)scales, M, K);
+                       (uint8_t *)scales, M, K, tiled);
     return check_launch("qim_mx_quantize");
 }
 
-extern "C" int qim_swiglu_quantize(const void *g, int64_t ldg, const void *v, int64_t ldv, void *q,
-                                   void *scales, int64_t M, int64_t F, void *stream) {
+static int swiglu_quantize(const void *g, int64_t ldg, const void *v, int64_t ldv, void *q, void *scales,
+                           int64_t M, int64_t F, int tiled, void *stream) {
     QIM_REQUIRE(g && v && q && scales, QIM_ERR_ARG, "qim_swiglu_quantize: null pointer");
     int rc = launch_quant_checks("qim_swiglu_quantize", M, F);
     if (rc) return rc;
@@ -133,6 +135,26 @@ extern "C" int qim_swiglu_quantize(const void *g, int64_t ldg, const void *v, in
     dim3 grid((unsigned)((M + 127) / 128), (unsigned)(F / 128));
     SwigluSource src{(const uint16_t *)g, ldg, (const uint16_t *)v, ldv};
     hipLaunchKernelGGL(k_quant_tile<SwigluSource>, grid, dim3(256), 0, as_stream(stream), src, (uint8_t *)q,
-                       (uint8_t *)scales, M, F);
+                       (uint8_t *)scales, M, F, tiled);
     return check_launch("qim_swiglu_quantize");
+}
+
+extern "C" int qim_mx_quantize(const void *x, int64_t ldx, int64_t M, int64_t K, void *q, void *scales,
+                               void *stream) {
+    return mx_quantize(x, ldx, M, K, q, scales, 0, stream);
+}
+
+extern "C" int qim_mx_quantize_tiled(const void *x, int64_t ldx, int64_t M, int64_t K, void *q, void *scales,
+                                     void *stream) {
+    return mx_quantize(x, ldx, M, K, q, scales, 1, stream);
+}
+
+extern "C" int qim_swiglu_quantize(const void *g, int64_t ldg, const void *v, int64_t ldv, void *q,
+                                   void *scales, int64_t M, int64_t F, void *stream) {
+    return swiglu_quantize(g, ldg, v, ldv, q, scales, M, F, 0, stream);
+}
+
+extern "C" int qim_swiglu_quantize_tiled(const void *g, int64_t ldg, const void *v, int64_t ldv, void *q,
+                                         void *scales, int64_t M, int64_t F, void *stream) {
+    return swiglu_quantize(g, ldg, v, ldv, q, scales, M, F, 1, stream);
 }

@@ -15,7 +15,8 @@ LIB_PATH = os.environ.get("QIM_LIBRARY", os.path.join(os.path.dirname(os.path.ab
                                                        "libqim.so"))
 
 QIM_OK, QIM_ERR_ARG, QIM_ERR_SHAPE, QIM_ERR_LAYOUT, QIM_ERR_LAUNCH = range(5)
-ADALN_ADD_ONE = 1
+ADALN_ADD_ONE, ADALN_TILED = 1, 2
+GEMM_A_TILED, GEMM_B_TILED, GEMM_OUT_TILED = 1, 2, 4
 EPI_NONE, EPI_BIAS, EPI_GATED_RESIDUAL, EPI_SWIGLU, EPI_SWIGLU_QUANT = range(5)
 SWIGLU_GROUP = 32
 
@@ -45,15 +46,18 @@ SIGNATURES = {
     "qim_last_error": (ctypes.c_char_p, []),
     "qim_abi_version": (_C, []),
     "qim_mx_quantize": (_C, [_P, _I, _I, _I, _P, _P, _P]),
+    "qim_mx_quantize_tiled": (_C, [_P, _I, _I, _I, _P, _P, _P]),
     "qim_adaln": (_C, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _C, _P]),
     "qim_adaln_quantize": (_C, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _C, _P]),
     "qim_gated_residual": (_C, [_P, _P, _P, _P, _I, _I, _I, _P]),
     "qim_swiglu": (_C, [_P, _I, _P, _I, _P, _I, _I, _I, _P]),
     "qim_swiglu_quantize": (_C, [_P, _I, _P, _I, _P, _P, _I, _I, _P]),
+    "qim_swiglu_quantize_tiled": (_C, [_P, _I, _P, _I, _P, _P, _I, _I, _P]),
     "qim_rms_norm": (_C, [_P, _P, _P, _I, _I, _F, _P]),
     "qim_rope_qk": (_C, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "qim_qk_norm_rope_pack": (_C, [_P] * 11 + [_I] * 6 + [_F, _F, _P]),
     "qim_mxfp8_gemm": (_C, [_P, _P, _P, _P, _I, _I, _I, _C, _P, _P, _P, _I, _P, _I, _P, _P]),
+    "qim_mxfp8_gemm_ex": (_C, [_P, _P, _P, _P, _I, _I, _I, _C, _C, _P, _P, _P, _I, _P, _I, _P, _P]),
     "qim_debug_e4m3_encode": (_C, [_P, _P, _I, _P]),
     "qim_debug_bf16_round": (_C, [_P, _P, _I, _P]),
     "qim_debug_mfma_tile": (_C, [_P, _P, _P, _P, _P, _P]),

@@ -15,7 +15,9 @@ modulation, fused QKV projection, hidden 3072, 24 heads x 128, FFN 12288):
     a   = MXFP8(silu(x @ W_gate) * (x @ W_up))              GEMM, SwiGLU->MXFP8 epilogue
     h   = h + tanh(g2) * (a @ W_down)                       GEMM, gated-residual epilogue
 
-Eight launches; every bf16 rounding point of the eager block is kept (the
+Eight launches; every MXFP8 operand (weights and activations) is in the GEMM's
+tiled code layout, written that way by its producer; every bf16 rounding point
+of the eager block is kept (the
 activation quantizations share one FP8 tensor per consumer group, as in
 quantized_decode.py:50-53, 81-96).  The modulation precompute (1 + s is done
 inside the LayerNorm kernel, tanh(g) in eager torch) is the reference's
@@ -46,10 +48,10 @@ class MMDiTBlock:
     dim: int
     heads: int
     ffn: int
-    w_qkv: mxfp8.Quantized      # (3*dim, dim)
-    w_out: mxfp8.Quantized      # (dim, dim)
-    w_gate_up: mxfp8.Quantized  # (2*ffn, dim), gate/up rows interleaved
-    w_down: mxfp8.Quantized     # (dim, ffn)
+    w_qkv: mxfp8.Quantized      # (3*dim, dim), tiled codes
+    w_out: mxfp8.Quantized      # (dim, dim), tiled codes
+    w_gate_up: mxfp8.Quantized  # (2*ffn, dim), gate/up rows interleaved, tiled codes
+    w_down: mxfp8.Quantized     # (dim, ffn), tiled codes
     norm_q: torch.Tensor        # (head_dim,) bf16
     norm_k: torch.Tensor
     bf16_weights: dict          # the unquantized bf16 weights (kept for checking)
@@ -61,8 +63,9 @@ class MMDiTBlock:
         dim = w_out.shape[0]
         ffn = w_gate.shape[0]
         gu = gemm.interleave_swiglu(w_gate, w_up)
-        return MMDiTBlock(dim, heads, ffn, mxfp8.quantize(w_qkv), mxfp8.quantize(w_out),
-                          mxfp8.quantize(gu), mxfp8.quantize(w_down), norm_q, norm_k,
+        def q(w):
+            return mxfp8.quantize(w, tiled=True)
+        return MMDiTBlock(dim, heads, ffn, q(w_qkv), q(w_out), q(gu), q(w_down), norm_q, norm_k,
                           dict(qkv=w_qkv, out=w_out, gate=w_gate, up=w_up, down=w_down,
                                norm_q=norm_q, norm_k=norm_k))
 
@@ -89,8 +92,8 @@ class MMDiTBlock:
         hd = d // self.heads
 
         x = layer_norm_scale_quantize(h, scale1.contiguous(), norm, shift=shift1.contiguous(),
-                                      add_one=True)
-        qkv = gemm.mx_matmul(x, self.w_qkv.values, self.w_qkv.scales)          # (B*S, 3d)
+                                      add_one=True, tiled=True)
+        qkv = self._mm(x, self.w_qkv)                                            # (B*S, 3d)
         qkv4 = qkv.view(b, s, 3 * d)
         q = qkv4[:, :, :d].unflatten(-1, (self.heads, hd))
         k = qkv4[:, :, d:2 * d].unflatten(-1, (self.heads, hd))
@@ -99,16 +102,20 @@ class MMDiTBlock:
             o = qkv[:, 2 * d:]                                                   # stand-in: v
         else:
             o = attention_fn(q, k, qkv4[:, :, 2 * d:].unflatten(-1, (self.heads, hd))).reshape(b * s, d)
-        oq = mxfp8.quantize(o)
-        h1 = gemm.mx_matmul(oq, self.w_out.values, self.w_out.scales, epilogue="gated_residual",
-                            gate=gate1.contiguous(), residual=h.reshape(b * s, d), seq=s)
+        oq = mxfp8.quantize(o, tiled=True)
+        h1 = self._mm(oq, self.w_out, epilogue="gated_residual", gate=gate1.contiguous(),
+                      residual=h.reshape(b * s, d), seq=s)
         h1 = h1.view(b, s, d)
         x2 = layer_norm_scale_quantize(h1, scale2.contiguous(), norm, shift=shift2.contiguous(),
-                                       add_one=True)
-        a = gemm.mx_matmul(x2, self.w_gate_up.values, self.w_gate_up.scales, epilogue="swiglu_quant")
-        h2 = gemm.mx_matmul(a, self.w_down.values, self.w_down.scales, epilogue="gated_residual",
-                            gate=gate2.contiguous(), residual=h1.reshape(b * s, d), seq=s)
+                                       add_one=True, tiled=True)
+        a = self._mm(x2, self.w_gate_up, epilogue="swiglu_quant", out_tiled=True)
+        h2 = self._mm(a, self.w_down, epilogue="gated_residual", gate=gate2.contiguous(),
+                      residual=h1.reshape(b * s, d), seq=s)
         return h2.view(b, s, d)
+
+    @staticmethod
+    def _mm(x, w, **epilogue):
+        return gemm.mx_matmul(x, w.values, w.scales, weight_tiled=True, **epilogue)
 
     def flops(self, tokens):
         """GEMM flops of one forward over `tokens` rows (2*M*N*K each)."""

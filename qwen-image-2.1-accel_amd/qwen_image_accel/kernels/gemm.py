@@ -43,25 +43,33 @@ def interleave_swiglu(gate_weight, up_weight, group=_native.SWIGLU_GROUP):
 
 
 def mx_matmul(activation, weight_fp8, weight_scale, *, epilogue="none", bias=None, gate=None,
-              residual=None, seq=None, out=None):
+              residual=None, seq=None, out=None, weight_tiled=False, out_tiled=False):
     """``activation @ weight.T`` in MXFP8 with a fused epilogue.
 
-    activation: ``Quantized`` (Mp, K).  weight_fp8: codes of the (N, K) weight
-    (or its (K, N) column-major view); weight_scale: its swizzled scales.
-    Returns bf16 (rows, N) -- (rows, N/2) for "swiglu" -- or a ``Quantized``
-    (rows, N/2) for "swiglu_quant".  ``gate`` is (B, 1, N) or (B, N) with
-    ``seq`` rows per batch; ``residual`` is (rows, N)."""
+    activation: ``Quantized`` (Mp, K), row-major or tiled (``TiledQuantized``).
+    weight_fp8: codes of the (N, K) weight (or its (K, N) column-major view), or
+    with ``weight_tiled=True`` the (N, K) codes in the tiled layout;
+    weight_scale: its swizzled scales.  Returns bf16 (rows, N) -- (rows, N/2)
+    for "swiglu" -- or a ``Quantized`` (rows, N/2) for "swiglu_quant"
+    (``TiledQuantized`` with ``out_tiled=True``).  ``gate`` is (B, 1, N) or
+    (B, N) with ``seq`` rows per batch; ``residual`` is (rows, N)."""
     epi = EPILOGUES[epilogue]
     a = activation
-    w = weight_rows(weight_fp8)
+    w = weight_fp8 if weight_tiled else weight_rows(weight_fp8)
+    if weight_tiled and not w.is_contiguous():
+        raise _native.Unsupported("mx_matmul", _native.QIM_ERR_LAYOUT, "tiled weight codes must be dense")
     n, k = w.shape
+    if out_tiled and epi != _native.EPI_SWIGLU_QUANT:
+        raise ValueError("out_tiled applies to the quantized SwiGLU epilogue only")
+    layouts = ((_native.GEMM_A_TILED if a.tiled else 0) | (_native.GEMM_B_TILED if weight_tiled else 0)
+               | (_native.GEMM_OUT_TILED if out_tiled else 0))
     if a.values.shape[1] != k:
         raise ValueError(f"activation K={a.values.shape[1]} does not match weight K={k}")
     m = a.rows
     dev = a.values.device
     out_scales = None
     if epi == _native.EPI_SWIGLU_QUANT:
-        result = empty_quantized(m, n // 2, dev)
+        result = empty_quantized(m, n // 2, dev, tiled=out_tiled)
         buf, ldo, out_scales = result.values, n // 2, result.scales
     else:
         width = n // 2 if epi == _native.EPI_SWIGLU else n
@@ -74,8 +82,8 @@ def mx_matmul(activation, weight_fp8, weight_scale, *, epilogue="none", bias=Non
         gate = gate.reshape(-1, n)
         if residual.shape != (m, n) or not residual.is_contiguous() or not gate.is_contiguous():
             raise ValueError("gated residual needs a contiguous (rows, N) residual and (B, N) gate")
-    _native.call("qim_mxfp8_gemm", _native.ptr(a.values), _native.ptr(a.scales), _native.ptr(w),
-                 _native.ptr(weight_scale), m, n, k, epi, _native.ptr(bias), _native.ptr(gate),
+    _native.call("qim_mxfp8_gemm_ex", _native.ptr(a.values), _native.ptr(a.scales), _native.ptr(w),
+                 _native.ptr(weight_scale), m, n, k, epi, layouts, _native.ptr(bias), _native.ptr(gate),
                  _native.ptr(residual), int(seq or m), _native.ptr(buf), ldo, _native.ptr(out_scales),
                  _native.stream(dev))
     return result

@@ -3,9 +3,13 @@
 Reference interface: src/qwen_image_accel/optimizations/mxfp8.py --
 ``MXFP8Linear`` (:19-41), ``LAYER_GROUPS`` (:46-50), ``selected_layers``
 (:53-63), ``quantize_transformer`` (:66-91).  Weights are quantized once with
-the same quantizer as activations and kept as the reference does: ``weight_fp8``
-is the (K, N) column-major view of the (N, K) codes, ``weight_scale`` the
-swizzled exponents over N rows.
+the same quantizer as activations.  The reference keeps ``weight_fp8`` = the
+(K, N) column-major view of the row-major (N, K) codes; here the same codes are
+kept once, in the GEMM's tiled layout (buffer ``weight_tiled``), so every DMA
+instruction of the GEMM reads 1 KiB contiguous.  ``weight_fp8`` remains
+readable (a row-major copy in the reference's view), and a state dict saved by
+the reference (``weight_fp8``) loads: its codes are tiled on the way in.
+``weight_scale`` is the swizzled exponents over N rows in both.
 """
 import os
 
@@ -13,7 +17,7 @@ import torch
 from torch import nn
 
 from qwen_image_accel.kernels.gemm import mx_matmul
-from qwen_image_accel.kernels.mxfp8 import Quantized, quantize
+from qwen_image_accel.kernels.mxfp8 import Quantized, quantize, tile_codes, untile_codes
 
 
 def _supported(k, n):
@@ -32,8 +36,8 @@ class MXFP8Linear(nn.Module):
             raise ValueError("Qwen 2.1 DiT MXFP8 conversion expects bias-free linears")
         self.in_features, self.out_features = linear.in_features, linear.out_features
         weight = linear.weight.detach().to(torch.bfloat16).contiguous()
-        quantized = quantize(weight)
-        self.register_buffer("weight_fp8", quantized.values.t())   # (K, N) column-major
+        quantized = quantize(weight, tiled=True)
+        self.register_buffer("weight_tiled", quantized.values)     # (N, K) codes, tiled layout
         self.register_buffer("weight_scale", quantized.scales)
         self.register_buffer("bias", None if linear.bias is None
                              else linear.bias.detach().to(torch.bfloat16).contiguous())
@@ -46,12 +50,24 @@ class MXFP8Linear(nn.Module):
             raise ValueError("the MXFP8 GEMM writes bfloat16")
         if self.bias is not None and "epilogue" not in epilogue:
             epilogue = dict(epilogue, epilogue="bias", bias=self.bias)
-        return mx_matmul(activation, self.weight_fp8, self.weight_scale, **epilogue)
+        return mx_matmul(activation, self.weight_tiled, self.weight_scale, weight_tiled=True, **epilogue)
 
     def forward(self, x):
         flat = x.reshape(-1, x.shape[-1])
-        activation = quantize(flat if flat.is_contiguous() else flat.contiguous())
+        activation = quantize(flat if flat.is_contiguous() else flat.contiguous(), tiled=True)
         return self.matmul(activation, x.dtype).reshape(*x.shape[:-1], self.out_features)
+
+    @property
+    def weight_fp8(self):
+        """The reference's view of the weight codes: (K, N) column-major (a copy)."""
+        return untile_codes(self.weight_tiled).t()
+
+    def _load_from_state_dict(self, state_dict, prefix, *args, **kwargs):
+        key = prefix + "weight_fp8"
+        if key in state_dict:  # a reference state dict: (K, N) view of row-major (N, K) codes
+            codes = state_dict.pop(key)
+            state_dict[prefix + "weight_tiled"] = tile_codes(codes.t() if codes.t().is_contiguous() else codes)
+        super()._load_from_state_dict(state_dict, prefix, *args, **kwargs)
 
 
 # Which of a block's linears each selection converts (reference :46-50).

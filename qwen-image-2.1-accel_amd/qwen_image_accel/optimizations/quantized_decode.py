@@ -4,7 +4,9 @@ Reference interface: src/qwen_image_accel/optimizations/quantized_decode.py --
 ``MXFusedProcessor`` (:31-78), ``_mx_mlp_forward`` (:81-96), ``_normalized``
 (:99-105), ``install_mx_fused_decode`` (:108-137).  Q/K/V share one quantized
 activation and the SwiGLU gate/value projections share another; LayerNorm and
-SwiGLU emit MXFP8 directly when every consumer is an MXFP8 linear.
+SwiGLU emit MXFP8 directly when every consumer is an MXFP8 linear.  Those
+shared activations are consumed only by this build's GEMM, so they are written
+in its tiled code layout.
 """
 import types
 
@@ -40,7 +42,7 @@ class MXFusedProcessor:
             lead = hidden_states.shape[:-1]
             q, k, v = (p.matmul(hidden_states).view(*lead, attn.heads, -1) for p in projections)
         elif all(isinstance(p, MXFP8Linear) for p in projections) and hidden_states.is_contiguous():
-            shared = quantize(hidden_states.reshape(-1, hidden_states.shape[-1]))
+            shared = quantize(hidden_states.reshape(-1, hidden_states.shape[-1]), tiled=True)
             lead = hidden_states.shape[:-1]
             q, k, v = (p.matmul(shared).view(*lead, attn.heads, -1) for p in projections)
         else:
@@ -55,12 +57,12 @@ def _mx_mlp_forward(self, hidden_states):
         shared = hidden_states
     elif (isinstance(self.gate_layer, MXFP8Linear) and isinstance(self.proj, MXFP8Linear)
             and hidden_states.is_contiguous()):
-        shared = quantize(hidden_states.reshape(-1, hidden_states.shape[-1]))
+        shared = quantize(hidden_states.reshape(-1, hidden_states.shape[-1]), tiled=True)
     else:
         return self.out(swiglu(self.gate_layer(hidden_states), self.proj(hidden_states)))
     gate, value = self.gate_layer.matmul(shared), self.proj.matmul(shared)
     if isinstance(self.out, MXFP8Linear):
-        activated = swiglu_quantize(gate, value)
+        activated = swiglu_quantize(gate, value, tiled=True)
         if activated is not None:
             return self.out.matmul(activated).view(*lead, -1)
     return self.out(swiglu(gate, value)).view(*lead, -1)
@@ -69,7 +71,7 @@ def _mx_mlp_forward(self, hidden_states):
 def _normalized(hidden_states, scale, norm, *consumers):
     """FP8 straight out of the LayerNorm when every consumer is an MXFP8 linear."""
     if all(isinstance(consumer, MXFP8Linear) for consumer in consumers):
-        fused = layer_norm_scale_quantize(hidden_states, scale, norm)
+        fused = layer_norm_scale_quantize(hidden_states, scale, norm, tiled=True)
         if fused is not None:
             return fused
     return layer_norm_scale(hidden_states, scale, norm)

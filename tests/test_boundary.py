@@ -129,7 +129,8 @@ def test_mxfp8_profile_matches_native_block(dev, monkeypatch):
     monkeypatch.setenv("QW21_MXFP8_SKIP_BLOCKS", "")
     cfg, used, err = _run_profile(dev, "mxfp8")
     assert cfg["mxfp8_linears"] == 14
-    assert {"qim_adaln_quantize", "qim_mxfp8_gemm", "qim_swiglu_quantize", "qim_mx_quantize"} <= used, used
+    assert {"qim_adaln_quantize", "qim_mxfp8_gemm_ex", "qim_swiglu_quantize_tiled",
+            "qim_mx_quantize_tiled"} <= used, used
     assert err < 5e-2, err
 
 

@@ -39,7 +39,7 @@ def test_single_hip_runtime():
 
 
 def test_abi_version():
-    assert _native.lib().qim_abi_version() == 1
+    assert _native.lib().qim_abi_version() == 2
 
 
 @pytest.mark.parametrize("name,args,code", [
@@ -58,6 +58,11 @@ def test_abi_version():
      _native.QIM_ERR_ARG),
     ("qim_mxfp8_gemm", (16, 16, 16, 16, 4, 256, 128, 2, None, None, None, 0, 16, 256, None, None),
      _native.QIM_ERR_ARG),
+    ("qim_mxfp8_gemm_ex", (16, 16, 16, 16, 4, 256, 128, 0, 8, None, None, None, 0, 16, 256, None, None),
+     _native.QIM_ERR_ARG),
+    ("qim_mxfp8_gemm_ex", (16, 16, 16, 16, 4, 256, 128, 0, 4, None, None, None, 0, 16, 256, None, None),
+     _native.QIM_ERR_ARG),
+    ("qim_mx_quantize_tiled", (16, 128, 1, 100, 16, 16, None), _native.QIM_ERR_SHAPE),
     ("qim_qk_norm_rope_pack", (16, 16, None, None, None, 16, 16, 16, 16, 16, None, 1, 4, 3, 2, 128,
                                256, 1e-6, 1e-6, None), _native.QIM_ERR_ARG),
 ])
