@@ -42,9 +42,18 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+SETTLE_MS = 30.0
+
+
 class Timed:
     """Capture `steps` calls of fn(i) (i = step index, for input rotation) in a
-    HIP graph, warm up, then time one replay with events."""
+    HIP graph, warm up, then time one replay with events.
+
+    Warm-up: at least `warmup` steps, and untimed replays until SETTLE_MS of
+    GPU time has passed.  Each component first builds its inputs on the host
+    while the GPU idles; the clocks then take ~20 ms of load to come back (a
+    bandwidth-bound kernel measured right away runs ~12% slow for the first
+    ~5 ms of replays, then holds its steady rate)."""
 
     def __init__(self, fn, steps, warmup):
         self.fn, self.steps, self.warmup = fn, steps, warmup
@@ -61,9 +70,17 @@ class Timed:
         with torch.cuda.graph(graph):
             for i in range(self.steps):
                 self.fn(i)
-        for _ in range(max(1, self.warmup // max(1, self.steps))):
+        for _ in range(max(1, -(-self.warmup // max(1, self.steps)))):
             graph.replay()
         torch.cuda.synchronize()
+        settled = 0.0
+        while settled < SETTLE_MS:
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            graph.replay()
+            b.record()
+            torch.cuda.synchronize()
+            settled += a.elapsed_time(b)
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         start.record()
@@ -262,12 +279,13 @@ def bench_block(tokens, steps, warmup):
                 gemm_frac=flops / us / 1e6 / MXFP8_PEAK_TFLOPS)
 
 
-def bench_copy(steps, warmup):
-    """A streaming device copy of 256 MiB (qim_debug_copy: one 16-byte
-    non-temporal load and store per lane): the achievable-bandwidth reference
-    and the calibration kernel of the FETCH_SIZE / WRITE_SIZE counters."""
+def bench_copy(steps, warmup, n=256 << 20, shape="256 MiB"):
+    """A streaming device copy of n bytes (qim_debug_copy: one 16-byte
+    non-temporal load and store per lane).  At 256 MiB: the achievable-bandwidth
+    reference and the calibration kernel of the FETCH_SIZE / WRITE_SIZE
+    counters; at the byte counts of configs 1 and 2: what one launch moving
+    that many bytes can reach at all."""
     from qwen_image_accel import _native
-    n = 256 << 20
     n_copies = copies_for(n)
     src = [torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1) for _ in range(n_copies)]
     dst = [torch.empty(n, dtype=torch.uint8, device="cuda") for _ in range(n_copies)]
@@ -277,9 +295,9 @@ def bench_copy(steps, warmup):
         j = i % n_copies
         rc = L.qim_debug_copy(src[j].data_ptr(), dst[j].data_ptr(), n, torch.cuda.current_stream().cuda_stream)
         assert rc == 0
-    us = Timed(step, max(10, steps // 10), warmup).run() * 1e3
+    us = Timed(step, max(10, steps // 10) if n >= (64 << 20) else steps, warmup).run() * 1e3
     return dict(kernel="k_debug_copy", us=us, bytes=2 * n, gbs=2 * n / us / 1e3, frac=2 * n / us / 1e3 / HBM_PEAK_GBS,
-                shape="256 MiB")
+                shape=shape)
 
 
 def measured_traffic(entry):
@@ -353,7 +371,10 @@ def main():
                      ("mxfp8_gemm_bias_1024_rowmajor", lambda: bench_gemm(steps, warm, tiled=False)),
                      ("block_1024", lambda: bench_block(4352, steps, warm)),
                      ("block_2048", lambda: bench_block(16640, steps, warm)),
-                     ("copy_256MiB", lambda: bench_copy(steps, warm))]:
+                     ("copy_256MiB", lambda: bench_copy(steps, warm)),
+                     # copies moving the algorithmic bytes of configs 1 and 2
+                     ("copy_23.6MB", lambda: bench_copy(steps, warm, 23611392 // 2, "23.6 MB moved")),
+                     ("copy_109MB", lambda: bench_copy(steps, warm, 109183488 // 2, "109.2 MB moved"))]:
         if not want(name):
             continue
         log(f"[bench] {name} ...")

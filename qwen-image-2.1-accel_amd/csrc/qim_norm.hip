@@ -265,13 +265,13 @@ struct NormRopeArgs {
 };
 
 // Head rows per lane of one wave: a wave owns U * (64 / (D / 8)) heads of one
-// tensor of one token (12 at D = 128 with U = 3).  Three 16-byte loads per
-// lane in flight was the fastest split of config 2 measured on MI355X (one
-// wave per token with all of its Q and K heads was 27% slower: every wave then
-// loads for the whole kernel's duration before its first store).  The launch
-// picks U in {3, 4, 2} so that the heads divide into whole waves (H = 24: 3;
-// H = 32: 4) and no lane tests its head index; other head counts take the
-// masked kernel with U = 3.
+// tensor of one token (8 at D = 128 with U = 2).  Measured on MI355X at
+// config 2 (steady-state clocks, rotating buffers): U = 2 19.4 us, U = 3
+// 19.6 us, U = 1 24-26 us, U = 6 (a whole tensor of a token per wave) 21.0 us;
+// a copy-only kernel of the same shape 19.3-19.7 us, so the arithmetic is
+// hidden.  The launch picks U in {2, 3, 4} so that the heads divide into whole
+// waves and no lane tests its head index; other head counts take the masked
+// kernel with U = 3.
 constexpr int NR_ROWS = 3;
 
 // Normalise (optionally) and rotate (optionally) one 8-value chunk of a head
@@ -410,9 +410,9 @@ static void launch_norm_rope_shape(NormRopeArgs a, int64_t prefix_blocks, hipStr
 template <int D, bool NORM, bool ROPE, int NTENS>
 static void launch_norm_rope_d(const NormRopeArgs &a, int64_t prefix_blocks, hipStream_t st) {
     constexpr int64_t RPI = 512 / D;
-    if (a.H % (3 * RPI) == 0) launch_norm_rope_shape<D, NORM, ROPE, NTENS, 3, true>(a, prefix_blocks, st);
+    if (a.H % (2 * RPI) == 0) launch_norm_rope_shape<D, NORM, ROPE, NTENS, 2, true>(a, prefix_blocks, st);
+    else if (a.H % (3 * RPI) == 0) launch_norm_rope_shape<D, NORM, ROPE, NTENS, 3, true>(a, prefix_blocks, st);
     else if (a.H % (4 * RPI) == 0) launch_norm_rope_shape<D, NORM, ROPE, NTENS, 4, true>(a, prefix_blocks, st);
-    else if (a.H % (2 * RPI) == 0) launch_norm_rope_shape<D, NORM, ROPE, NTENS, 2, true>(a, prefix_blocks, st);
     else launch_norm_rope_shape<D, NORM, ROPE, NTENS, NR_ROWS, false>(a, prefix_blocks, st);
 }
 
