@@ -204,6 +204,30 @@ __device__ __forceinline__ double group_sum(double v) {
     return v;
 }
 
+// Total over the 64 lanes of a wave, returned wave-uniform, without LDS: the
+// 16-lane rows reduce by DPP (every lane then holds its row's total), DPP
+// row_bcast:15 adds the last lane of rows 0 and 2 into rows 1 and 3, and
+// row_bcast:31 adds lane 31 into rows 2 and 3, so lane 63 holds the total.
+// Lanes of rows a broadcast does not write add 0.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ double dpp_bcast(double v) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint64_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, ROW_MASK, 0xF, false);
+    const uint64_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, ROW_MASK, 0xF, false);
+    return __builtin_bit_cast(double, lo | (hi << 32));
+}
+constexpr int DPP_ROW_BCAST15 = 0x142, DPP_ROW_BCAST31 = 0x143;
+
+__device__ __forceinline__ double wave_total(double v) {
+    v = group_sum<16>(v);
+    v += dpp_bcast<DPP_ROW_BCAST15, 0xA>(v);
+    v += dpp_bcast<DPP_ROW_BCAST31, 0xC>(v);
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, 63);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), 63);
+    return __builtin_bit_cast(double, (uint64_t)lo | ((uint64_t)hi << 32));
+}
+
 // Reciprocal square root of (var + eps) as the normalisations' reference
 // statistics define it: t = var + eps in fp32, then R = fp32(1 / sqrt(t))
 // evaluated in float64 (IEEE sqrt and divide) and rounded once.

@@ -608,18 +608,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     epilogue<EPI, 4, 4>(p, acc, lds, m0 + wm * 128, n0 + wn * 128, lane, wave);
 }
 
-// Compute units of the current device, cached per device (0 if unknown).
-static int device_cus() {
-    static int cached[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
-    if (dev < 64 && cached[dev]) return cached[dev];
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    if (dev < 64) cached[dev] = n;
-    return n;
-}
-
 // Whole tiles to launch: all of them, or all but the last r when the last
 // round of the CUs would hold r <= CUs / 2 tiles (those become 4r quarters).
 static int64_t main_tile_count(int64_t tiles) {

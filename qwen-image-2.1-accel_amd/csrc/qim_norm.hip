@@ -135,7 +135,7 @@ __global__ __launch_bounds__(FULL ? 64 * ADALN_FULL_WAVES : 64 * ADALN_MAX_WAVES
     for (int i = 0; i < NV; ++i)
 #pragma unroll
         for (int t = 0; t < 8; ++t) s += (double)x[i][t];
-    s = group_sum<64>(s);
+    s = wave_total(s);
     if (lane == 0) red[0][wave] = s;
     __syncthreads();
     s = 0.0;
@@ -151,7 +151,7 @@ __global__ __launch_bounds__(FULL ? 64 * ADALN_FULL_WAVES : 64 * ADALN_MAX_WAVES
             ss += d * d;
         }
     }
-    ss = group_sum<64>(ss);
+    ss = wave_total(ss);
     if (lane == 0) red[1][wave] = ss;
     __syncthreads();
     ss = 0.0;

@@ -18,6 +18,9 @@ inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Compute units of the current device, cached per device (0 if unknown).
+int device_cus();
+
 }  // namespace qim
 
 #define QIM_REQUIRE(cond, code, ...)                 \

@@ -24,6 +24,17 @@ int check_launch(const char *what) {
     return QIM_OK;
 }
 
+int device_cus() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+    if (dev < 64 && cached[dev]) return cached[dev];
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    if (dev < 64) cached[dev] = n;
+    return n;
+}
+
 // ----------------------------------------------------------- test hooks ----
 
 __global__ void k_debug_e4m3(const float *__restrict__ x, uint8_t *__restrict__ codes, int64_t n) {
