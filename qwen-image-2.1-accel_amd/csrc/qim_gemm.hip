@@ -39,7 +39,10 @@ constexpr int TILE_BYTES = BM * BK;                          // 16 KiB per opera
 constexpr int SCALE_BYTES = 1024;                            // two 512-byte chunks per operand
 constexpr int STAGE_BYTES = 2 * TILE_BYTES + 2 * SCALE_BYTES;  // 34 KiB
 constexpr int LDS_BYTES = NSTAGE * STAGE_BYTES;              // 136 KiB
-constexpr int LOADS_PER_STAGE = 10;                          // per wave: 4 A + 4 B (16 B) + 2 scale (4 B)
+// Loads per wave per stage: 4 A + 4 B (16 B each), plus 2 of 4 B for the
+// scales in even stages only: a 128-K scale group spans two stages, and odd
+// stages reuse the even stage's scales from registers.
+constexpr int LOADS_EVEN = 10, LOADS_ODD = 8;
 
 struct GemmArgs {
     const uint8_t *aq, *as, *bq, *bs;
@@ -151,6 +154,7 @@ __device__ __forceinline__ uint32_t lds_addr(const uint8_t *p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)p;
 }
 
+template <bool SCALES>
 __device__ __forceinline__ void issue_stage(const GemmArgs &p, const LoadPlan &L, uint8_t *slot, int s) {
     const uint32_t ka = (uint32_t)s * L.astep, kb = (uint32_t)s * L.bstep;
     const uint32_t base = lds_addr(slot);
@@ -158,10 +162,12 @@ __device__ __forceinline__ void issue_stage(const GemmArgs &p, const LoadPlan &L
     for (int j = 0; j < 4; ++j) dma16(p.aq, L.a[j] + ka, base + (L.wave * 4 + j) * 1024);
 #pragma unroll
     for (int j = 0; j < 4; ++j) dma16(p.bq, L.b[j] + kb, base + TILE_BYTES + (L.wave * 4 + j) * 1024);
-    const uint32_t gofs = (uint32_t)(s >> 1) * 512;
+    if constexpr (SCALES) {
+        const uint32_t gofs = (uint32_t)(s >> 1) * 512;
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-        dma4(L.sc_base[j], L.sc[j] + gofs, base + 2 * TILE_BYTES + (L.wave * 2 + j) * 256);
+        for (int j = 0; j < 2; ++j)
+            dma4(L.sc_base[j], L.sc[j] + gofs, base + 2 * TILE_BYTES + (L.wave * 2 + j) * 256);
+    }
 }
 
 struct Frags {
@@ -193,10 +199,10 @@ __device__ __forceinline__ void read_frags(const uint8_t *slot, int wm, int wn, 
     f.sb = read_scales(slot + 2 * TILE_BYTES + SCALE_BYTES, wn, lr);
 }
 
-// Every stage issues its 10 loads unconditionally (past the end of K they
+// Every stage issues its loads unconditionally (past the end of K they
 // re-read the last stage into a ring slot that is never read again), so at
 // the top of stage s the outstanding loads are always those of stages s+1,
-// s+2, s+3, and "stage s+1 landed" is always vmcnt(20).  Keeping the stage
+// s+2, s+3, and "stage s+1 landed" is always vmcnt(LOADS_EVEN + LOADS_ODD).  Keeping the stage
 // free of branches keeps it one basic block, which the explicit schedule
 // below needs.
 
@@ -239,7 +245,7 @@ __device__ __forceinline__ void pipeline_step(const GemmArgs &p, const LoadPlan 
 #define QIM_STEP(mi, mj, work) QIM_MF(mi, mj); QIM_SCHED(); work; QIM_SCHED()
     QIM_MF(0, 0);
     QIM_SCHED();
-    wait_vmcnt<2 * LOADS_PER_STAGE>();
+    wait_vmcnt<LOADS_EVEN + LOADS_ODD>();
     block_barrier();
     QIM_SCHED();
     QIM_STEP(0, 1, dma16(p.aq, L.a[0] + ka, fb + (w4 + 0) * 1024));
@@ -258,9 +264,10 @@ __device__ __forceinline__ void pipeline_step(const GemmArgs &p, const LoadPlan 
              nxt.b[2] = read_tile(next + TILE_BYTES, rb0 + 64, kh));
     QIM_STEP(2, 0, dma16(p.bq, L.b[3] + kb, fb + TILE_BYTES + (w4 + 3) * 1024);
              nxt.b[3] = read_tile(next + TILE_BYTES, rb0 + 96, kh));
-    QIM_STEP(2, 1, dma4(scb0, L.sc[0] + gofs, fb + 2 * TILE_BYTES + (L.wave * 2 + 0) * 256);
+    // Logical stage s + 4 has this stage's parity: scales in even stages only.
+    QIM_STEP(2, 1, if constexpr (PAR == 0) dma4(scb0, L.sc[0] + gofs, fb + 2 * TILE_BYTES + (L.wave * 2 + 0) * 256);
              nxt.a[1] = read_tile(next, ra0 + 32, kh));
-    QIM_STEP(2, 2, dma4(scb1, L.sc[1] + gofs, fb + 2 * TILE_BYTES + (L.wave * 2 + 1) * 256);
+    QIM_STEP(2, 2, if constexpr (PAR == 0) dma4(scb1, L.sc[1] + gofs, fb + 2 * TILE_BYTES + (L.wave * 2 + 1) * 256);
              nxt.a[2] = read_tile(next, ra0 + 64, kh));
     QIM_STEP(2, 3, nxt.a[3] = read_tile(next, ra0 + 96, kh));
     QIM_MF(3, 0);
@@ -440,7 +447,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
 // one.  A quarter tile: 4 waves in a 2 x 2 grid, each a 64 x 64 block of 2 x 2
 // MFMA tiles, on the same 4-stage LDS ring (half of each operand area used)
 // with the same schedule rules.
-constexpr int QLOADS = 5;  // per wave per stage: 2 A + 2 B (16 B) + 1 scale (4 B)
+constexpr int QLOADS_EVEN = 5, QLOADS_ODD = 4;  // per wave per stage: 2 A + 2 B (16 B) + 1 scale (4 B, even stages)
 
 struct QPlan {
     uint32_t a[2], b[2];   // byte offsets into aq / bq (stage 0)
@@ -470,14 +477,16 @@ __device__ __forceinline__ QPlan make_qplan(const GemmArgs &p, int64_t m0, int64
     return Q;
 }
 
+template <bool SCALES>
 __device__ __forceinline__ void issue_qstage(const GemmArgs &p, const QPlan &Q, uint8_t *slot, int s) {
     const uint32_t ka = (uint32_t)s * Q.astep, kb = (uint32_t)s * Q.bstep, base = lds_addr(slot), w2 = Q.wave * 2;
     dma16(p.aq, Q.a[0] + ka, base + (w2 + 0) * 1024);
     dma16(p.aq, Q.a[1] + ka, base + (w2 + 1) * 1024);
     dma16(p.bq, Q.b[0] + kb, base + TILE_BYTES + (w2 + 0) * 1024);
     dma16(p.bq, Q.b[1] + kb, base + TILE_BYTES + (w2 + 1) * 1024);
-    dma4(Q.sc_base, Q.sc + (uint32_t)(s >> 1) * 512,
-         base + 2 * TILE_BYTES + (Q.wave < 2 ? 0 : SCALE_BYTES) + (Q.wave & 1) * 256);
+    if constexpr (SCALES)
+        dma4(Q.sc_base, Q.sc + (uint32_t)(s >> 1) * 512,
+             base + 2 * TILE_BYTES + (Q.wave < 2 ? 0 : SCALE_BYTES) + (Q.wave & 1) * 256);
 }
 
 struct QFrags {
@@ -514,10 +523,10 @@ __device__ __forceinline__ void qstep(const GemmArgs &p, const QPlan &Q, uint8_t
                                                                 sa[i], PAR * 2, sb[j])
     QIM_QMF(0, 0);
     QIM_SCHED();
-    wait_vmcnt<2 * QLOADS>();
+    wait_vmcnt<QLOADS_EVEN + QLOADS_ODD>();
     block_barrier();
     QIM_SCHED();
-    issue_qstage(p, Q, lds + (s & 3) * STAGE_BYTES, s + 4 < S ? s + 4 : S - 1);
+    issue_qstage<PAR == 0>(p, Q, lds + (s & 3) * STAGE_BYTES, s + 4 < S ? s + 4 : S - 1);
     QIM_SCHED();
     QIM_QMF(0, 1);
     QIM_SCHED();
@@ -551,9 +560,11 @@ __device__ __forceinline__ void quarter_tile(const GemmArgs &p, uint8_t *lds, in
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = f32x16_t{};
     const QPlan Q = make_qplan(p, m0, n0);
-#pragma unroll
-    for (int i = 0; i < NSTAGE; ++i) issue_qstage(p, Q, lds + i * STAGE_BYTES, i < S ? i : S - 1);
-    wait_vmcnt<3 * QLOADS>();  // stage 0 landed
+    issue_qstage<true>(p, Q, lds, 0);
+    issue_qstage<false>(p, Q, lds + STAGE_BYTES, 1 < S ? 1 : S - 1);
+    issue_qstage<true>(p, Q, lds + 2 * STAGE_BYTES, 2 < S ? 2 : S - 1);
+    issue_qstage<false>(p, Q, lds + 3 * STAGE_BYTES, 3 < S ? 3 : S - 1);
+    wait_vmcnt<QLOADS_ODD + QLOADS_EVEN + QLOADS_ODD>();  // stage 0 landed
     block_barrier();
     QFrags fa, fb;
     read_qfrags(lds, wm, wn, lr, kh, fa, true);
@@ -589,9 +600,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
 
     const LoadPlan L = make_plan(p, m0, n0);
-#pragma unroll
-    for (int i = 0; i < NSTAGE; ++i) issue_stage(p, L, lds + i * STAGE_BYTES, i < S ? i : S - 1);
-    wait_vmcnt<3 * LOADS_PER_STAGE>();  // stage 0 landed
+    issue_stage<true>(p, L, lds, 0);
+    issue_stage<false>(p, L, lds + STAGE_BYTES, 1 < S ? 1 : S - 1);
+    issue_stage<true>(p, L, lds + 2 * STAGE_BYTES, 2 < S ? 2 : S - 1);
+    issue_stage<false>(p, L, lds + 3 * STAGE_BYTES, 3 < S ? 3 : S - 1);
+    wait_vmcnt<LOADS_ODD + LOADS_EVEN + LOADS_ODD>();  // stage 0 landed
     block_barrier();
     Frags fa, fb;
     read_frags(lds, wm, wn, lr, kh, fa);
