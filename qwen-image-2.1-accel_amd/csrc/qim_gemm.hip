@@ -415,14 +415,14 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
                     c.y = cvt_e4m3x4(f[4] * inv, f[5] * inv, f[6] * inv, f[7] * inv);
                     if (grow < p.Mp) {
                         const int64_t o = p.out_tiled ? mxt_offset(grow, col, p.Mp, F) : grow * F + col;
-                        *reinterpret_cast<uint2 *>(reinterpret_cast<uint8_t *>(p.out) + o) = c;
+                        st_nt(reinterpret_cast<uint8_t *>(p.out) + o, c);
                         if ((cl & 3) == 0) p.out_scales[mx_scale_offset(grow, col >> 5, F)] = (uint8_t)e;
                     }
                 } else {
                     if (grow >= p.M) continue;
                     uint4 o = v;
                     if constexpr (EPI == QIM_EPI_GATED_RESIDUAL) {
-                        const uint4 hv = *reinterpret_cast<const uint4 *>(p.res + grow * p.N + col);
+                        const uint4 hv = ld_nt(p.res + grow * p.N + col);
                         const uint4 gv = *reinterpret_cast<const uint4 *>(p.gate + (grow / p.seq) * p.N + col);
                         float y[8], h[8], gg[8], z[8];
                         unpack8(v, y);
@@ -432,7 +432,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
                         for (int t = 0; t < 8; ++t) z[t] = h[t] + rbf(gg[t] * y[t]);
                         o = pack8(z);
                     }
-                    *reinterpret_cast<uint4 *>(reinterpret_cast<uint16_t *>(p.out) + grow * p.ldo + col) = o;
+                    st_nt(reinterpret_cast<uint16_t *>(p.out) + grow * p.ldo + col, o);
                 }
             }
         }
