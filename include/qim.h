@@ -44,6 +44,8 @@ enum qim_epilogue {
     QIM_EPI_GATED_RESIDUAL = 2, /* out = bf16(res + bf16(gate[b, n] * bf16(acc)))      */
     QIM_EPI_SWIGLU = 3,         /* out[m, j] = swiglu(bf16(acc_gate), bf16(acc_up))    */
     QIM_EPI_SWIGLU_QUANT = 4,   /* MXFP8 codes + scales of the QIM_EPI_SWIGLU output   */
+    QIM_EPI_QK_NORM_ROPE = 5,   /* QKV projection with per-head RMSNorm + RoPE of Q, K
+                                   (qim_mxfp8_gemm_qk_norm_rope only)                  */
 };
 
 /* Rows of the gate and of the up projection alternate in groups of this many
@@ -171,6 +173,19 @@ int qim_mxfp8_gemm_ex(const void *aq, const void *as, const void *bq, const void
                       int64_t M, int64_t N, int64_t K, int epilogue, int layouts,
                       const void *bias, const void *gate, const void *res, int64_t seq,
                       void *out, int64_t ldo, void *out_scales, void *stream);
+
+/* The fused QKV projection of the MMDiT block: qim_mxfp8_gemm_ex with
+ * N = 3 * H * 128 whose output columns [0, H*128) (Q) and [H*128, 2*H*128) (K)
+ * leave the GEMM as rope(RMSNorm(bf16(acc))) per 128-wide head, exactly what
+ * qim_qk_norm_rope_pack (P = 0, no V) computes on the unfused output; columns
+ * [2*H*128, 3*H*128) (V) are bf16(acc).  wq, wk: (128,) bf16; freqs:
+ * (seq, 64) complex64 as interleaved fp32, row = output row % seq.  out: bf16
+ * (M, N), row stride ldo.  H even.  Fuses kernels/attention.py:16-89 (P = 0)
+ * into optimizations/mxfp8.py:32-36. */
+int qim_mxfp8_gemm_qk_norm_rope(const void *aq, const void *as, const void *bq, const void *bs,
+                                int64_t M, int64_t K, int64_t H, int layouts, const void *wq,
+                                const void *wk, const void *freqs, int64_t seq, float epsq,
+                                float epsk, void *out, int64_t ldo, void *stream);
 
 /* Test hooks: the device conversions every kernel uses, applied elementwise
  * (fp32 -> E4M3 code; fp32 -> bf16 bits), and one scaled MFMA

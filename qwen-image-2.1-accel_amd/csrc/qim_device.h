@@ -250,6 +250,50 @@ __device__ __forceinline__ float rstd_of(float var, float eps) {
     return (float)(1.0 / sqrt(td));
 }
 
+// Per-head RMSNorm + RoPE of one 8-value chunk of a head row (Diffusers
+// RMSNorm: n = bf16(x * rsqrt(mean(x^2) + eps)), out = bf16(n * w); then the
+// complex rotation of the pairs (x[2j], x[2j+1]), reference
+// kernels/bf16.py:52-55 and kernels/elementwise.py:53-56).
+//
+// The sum of squares is taken in float64: for bf16 inputs it is exact, so it
+// does not depend on how the lanes of a row are reduced; it is rounded once to
+// the fp32 mean.
+__device__ __forceinline__ double head_sumsq8(const float *x) {
+    double ss = 0.0;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) ss += (double)x[t] * (double)x[t];
+    return ss;
+}
+// x: the chunk; ss: the row's total sum of squares over `width` values; w: the
+// chunk's 8 weights.  Roundings are paired (one v_cvt_pk_bf16_f32 per two).
+__device__ __forceinline__ void head_rmsnorm8(float *x, double ss, int width, float eps, const float *w) {
+    const float r = rstd_of((float)(ss / (double)width), eps);
+#pragma unroll
+    for (int t = 0; t < 8; t += 2) {
+        float a = x[t] * r, b = x[t + 1] * r;
+        rbf2(a, b);
+        a *= w[t];
+        b *= w[t + 1];
+        rbf2(a, b);
+        x[t] = a;
+        x[t + 1] = b;
+    }
+}
+// f0, f1: the (cos, sin) pairs of the chunk's 4 complex positions.  Same FMA
+// order as the CUDA complex multiply the reference keeps.
+__device__ __forceinline__ void head_rope8(float *x, const float4 &f0, const float4 &f1) {
+    const float c[4] = {f0.x, f0.z, f1.x, f1.z};
+    const float s[4] = {f0.y, f0.w, f1.y, f1.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float xr = x[2 * j], xi = x[2 * j + 1];
+        const float re = __builtin_fmaf(xr, c[j], -(xi * s[j]));
+        const float im = __builtin_fmaf(xi, c[j], xr * s[j]);
+        x[2 * j] = re;
+        x[2 * j + 1] = im;
+    }
+}
+
 template <int WIDTH>
 __device__ __forceinline__ uint32_t group_umax(uint32_t v) {
     uint32_t o;

@@ -55,6 +55,12 @@ struct GemmArgs {
     int tiles_m, tiles_n;
     int main_tiles;  // whole tiles; workgroups past them compute quarter tiles of the rest
     int a_tiled, b_tiled, out_tiled;  // code layouts (mxt_offset) of A, B and a quantized output
+    // QIM_EPI_QK_NORM_ROPE: head weights, RoPE table (seq rows of 128 fp32),
+    // and the column ends of Q (H * 128) and K (2 * H * 128).
+    const uint16_t *wq, *wk;
+    const float *freqs;
+    float epsq, epsk;
+    int64_t q_cols, qk_cols;
 };
 
 __device__ __forceinline__ int kswz(int row) { return mx_chunk_swizzle(row); }
@@ -400,6 +406,47 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
                 for (int r = 0; r < 4; ++r) rowv[r] = make_uint4(w[r][0], w[r][1], w[r][2], w[r][3]);
             }
             const int64_t col = col0 + cl * 8;
+            if constexpr (EPI == QIM_EPI_QK_NORM_ROPE) {
+                // Q and K head columns: RMSNorm + RoPE of each row's 128-wide
+                // head, as k_norm_rope computes it on the stored output.  A
+                // wave holds W columns of the head; with W = 64 (quarter tiles)
+                // the other half is the partner wave's (wave ^ 1, same rows),
+                // whose row sums come through LDS.  The Q/K/V class is uniform
+                // over a quarter tile's four waves (one head), so its barriers
+                // are too.
+                if (col0 < p.qk_cols) {
+                    const bool isq = col0 < p.q_cols;
+                    const int hc = (int)(col0 & 127) + cl * 8;  // column within the head
+                    float wt[8], x[4][8];
+                    double ss[4];
+                    unpack8(*reinterpret_cast<const uint4 *>((isq ? p.wq : p.wk) + hc), wt);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        unpack8(rowv[r], x[r]);
+                        ss[r] = group_sum<LPR>(head_sumsq8(x[r]));
+                    }
+                    if constexpr (W < 128) {
+                        static_assert(W == 64, "a head spans two waves at most");
+                        double *xs = reinterpret_cast<double *>(lds + 4 * 16 * RGS) + (it & 1) * (4 * GPI * 4);
+                        if (cl == 0) {
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) xs[(wave * GPI + gl) * 4 + r] = ss[r];
+                        }
+                        __syncthreads();
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) ss[r] += xs[((wave ^ 1) * GPI + gl) * 4 + r];
+                    }
+                    const float eps = isq ? p.epsq : p.epsk;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const uint32_t tok = (uint32_t)(row0 + half * 64 + 4 * g + r) % (uint32_t)p.seq;
+                        const float4 *fr = reinterpret_cast<const float4 *>(p.freqs + (int64_t)tok * 128 + hc);
+                        head_rmsnorm8(x[r], ss[r], 128, eps, wt);
+                        head_rope8(x[r], fr[0], fr[1]);
+                        rowv[r] = pack8(x[r]);
+                    }
+                }
+            }
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int64_t grow = row0 + half * 64 + 4 * g + r;
@@ -650,10 +697,16 @@ static int launch_gemm(const GemmArgs &a, int64_t tiles, hipStream_t st) {
 
 using namespace qim;
 
-extern "C" int qim_mxfp8_gemm_ex(const void *aq, const void *as, const void *bq, const void *bs, int64_t M,
-                                 int64_t N, int64_t K, int epilogue, int layouts, const void *bias, const void *gate,
-                                 const void *res, int64_t seq, void *out, int64_t ldo, void *out_scales,
-                                 void *stream) {
+// Operands of the QK-norm-RoPE epilogue (qim_mxfp8_gemm_qk_norm_rope).
+struct QKNormRope {
+    const void *wq, *wk, *freqs;
+    float epsq, epsk;
+    int64_t heads;
+};
+
+static int gemm_run(const void *aq, const void *as, const void *bq, const void *bs, int64_t M, int64_t N, int64_t K,
+                    int epilogue, int layouts, const void *bias, const void *gate, const void *res, int64_t seq,
+                    void *out, int64_t ldo, void *out_scales, const QKNormRope *qk, void *stream) {
     QIM_REQUIRE(aq && as && bq && bs && out, QIM_ERR_ARG, "qim_mxfp8_gemm: null pointer");
     QIM_REQUIRE((layouts & ~(QIM_GEMM_A_TILED | QIM_GEMM_B_TILED | QIM_GEMM_OUT_TILED)) == 0, QIM_ERR_ARG,
                 "qim_mxfp8_gemm: unknown layout flags 0x%x", layouts);
@@ -676,7 +729,17 @@ extern "C" int qim_mxfp8_gemm_ex(const void *aq, const void *as, const void *bq,
                (const uint16_t *)bias, (const uint16_t *)gate, (const uint16_t *)res, seq > 0 ? seq : M, out, ldo,
                (uint8_t *)out_scales, (int)tiles_m, (int)tiles_n, 0,
                (layouts & QIM_GEMM_A_TILED) != 0, (layouts & QIM_GEMM_B_TILED) != 0,
-               (layouts & QIM_GEMM_OUT_TILED) != 0};
+               (layouts & QIM_GEMM_OUT_TILED) != 0,
+               nullptr, nullptr, nullptr, 0.0f, 0.0f, 0, 0};
+    if (qk) {
+        a.wq = (const uint16_t *)qk->wq;
+        a.wk = (const uint16_t *)qk->wk;
+        a.freqs = (const float *)qk->freqs;
+        a.epsq = qk->epsq;
+        a.epsk = qk->epsk;
+        a.q_cols = qk->heads * 128;
+        a.qk_cols = 2 * qk->heads * 128;
+    }
     const int64_t tiles = tiles_m * tiles_n;
     a.main_tiles = (int)main_tile_count(tiles);
     int rc;
@@ -705,6 +768,11 @@ extern "C" int qim_mxfp8_gemm_ex(const void *aq, const void *as, const void *bq,
             QIM_REQUIRE(out_scales, QIM_ERR_ARG, "qim_mxfp8_gemm: quantized output needs out_scales");
             rc = launch_gemm<QIM_EPI_SWIGLU_QUANT>(a, tiles, as_stream(stream));
             break;
+        case QIM_EPI_QK_NORM_ROPE:
+            QIM_REQUIRE(qk, QIM_ERR_ARG, "qim_mxfp8_gemm: the QK epilogue is qim_mxfp8_gemm_qk_norm_rope's");
+            QIM_REQUIRE(ldo >= N, QIM_ERR_LAYOUT, "qim_mxfp8_gemm: ldo=%lld < N", (long long)ldo);
+            rc = launch_gemm<QIM_EPI_QK_NORM_ROPE>(a, tiles, as_stream(stream));
+            break;
         default:
             return fail(QIM_ERR_ARG, "qim_mxfp8_gemm: unknown epilogue %d", epilogue);
     }
@@ -716,4 +784,30 @@ extern "C" int qim_mxfp8_gemm(const void *aq, const void *as, const void *bq, co
                               int64_t seq, void *out, int64_t ldo, void *out_scales, void *stream) {
     return qim_mxfp8_gemm_ex(aq, as, bq, bs, M, N, K, epilogue, 0, bias, gate, res, seq, out, ldo, out_scales,
                              stream);
+}
+
+extern "C" int qim_mxfp8_gemm_ex(const void *aq, const void *as, const void *bq, const void *bs, int64_t M,
+                                 int64_t N, int64_t K, int epilogue, int layouts, const void *bias, const void *gate,
+                                 const void *res, int64_t seq, void *out, int64_t ldo, void *out_scales,
+                                 void *stream) {
+    return gemm_run(aq, as, bq, bs, M, N, K, epilogue, layouts, bias, gate, res, seq, out, ldo, out_scales, nullptr,
+                    stream);
+}
+
+extern "C" int qim_mxfp8_gemm_qk_norm_rope(const void *aq, const void *as, const void *bq, const void *bs,
+                                           int64_t M, int64_t K, int64_t H, int layouts, const void *wq,
+                                           const void *wk, const void *freqs, int64_t seq, float epsq, float epsk,
+                                           void *out, int64_t ldo, void *stream) {
+    QIM_REQUIRE(wq && wk && freqs, QIM_ERR_ARG, "qim_mxfp8_gemm_qk_norm_rope: null pointer");
+    QIM_REQUIRE(H > 0 && H % 2 == 0 && H < (1 << 20), QIM_ERR_SHAPE,
+                "qim_mxfp8_gemm_qk_norm_rope: H=%lld must be even (N = 3 H 128 %% 256 == 0)", (long long)H);
+    QIM_REQUIRE(seq > 0 && seq < (1ll << 31) && M < (1ll << 31), QIM_ERR_SHAPE,
+                "qim_mxfp8_gemm_qk_norm_rope: seq=%lld / M=%lld out of range", (long long)seq, (long long)M);
+    QIM_REQUIRE(aligned16(wq) && aligned16(wk) && aligned16(freqs), QIM_ERR_LAYOUT,
+                "qim_mxfp8_gemm_qk_norm_rope: wq, wk, freqs must be 16-byte aligned");
+    QIM_REQUIRE((layouts & QIM_GEMM_OUT_TILED) == 0, QIM_ERR_ARG,
+                "qim_mxfp8_gemm_qk_norm_rope: the output is bf16 (no tiled output)");
+    const QKNormRope qk{wq, wk, freqs, epsq, epsk, H};
+    return gemm_run(aq, as, bq, bs, M, 3 * H * 128, K, QIM_EPI_QK_NORM_ROPE, layouts, nullptr, nullptr, nullptr, seq,
+                    out, ldo, nullptr, &qk, stream);
 }

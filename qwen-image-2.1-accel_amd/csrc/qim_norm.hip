@@ -275,48 +275,18 @@ struct NormRopeArgs {
 constexpr int NR_ROWS = 3;
 
 // Normalise (optionally) and rotate (optionally) one 8-value chunk of a head
-// row; LPR lanes share the row.  Roundings are paired (one v_cvt_pk_bf16_f32
-// per two values).
+// row; LPR lanes share the row (the helpers are in qim_device.h).
 template <int LPR, bool NORM, bool ROPE>
 __device__ __forceinline__ uint4 norm_rope_chunk(const uint4 &xv, const float *w, float eps, const float4 &f0,
                                                  const float4 &f1) {
     float x[8];
     unpack8(xv, x);
     if constexpr (NORM) {
-        // Sum of squares in float64: exact for bf16 inputs, so independent of
-        // the reduction order; rounded once to the fp32 mean.
-        double ss = 0.0;
-#pragma unroll
-        for (int t = 0; t < 8; ++t) ss += (double)x[t] * (double)x[t];
-        ss = group_sum<LPR>(ss);
-        const float r = rstd_of((float)(ss / (double)(LPR * 8)), eps);
-#pragma unroll
-        for (int t = 0; t < 8; t += 2) {
-            float a = x[t] * r, b = x[t + 1] * r;
-            rbf2(a, b);
-            a *= w[t];
-            b *= w[t + 1];
-            rbf2(a, b);
-            x[t] = a;
-            x[t + 1] = b;
-        }
+        const double ss = group_sum<LPR>(head_sumsq8(x));
+        head_rmsnorm8(x, ss, LPR * 8, eps, w);
     }
-    if constexpr (ROPE) {
-        const float c[4] = {f0.x, f0.z, f1.x, f1.z};
-        const float s[4] = {f0.y, f0.w, f1.y, f1.w};
-        float o[8];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float xr = x[2 * j], xi = x[2 * j + 1];
-            // Same FMA order as the CUDA complex multiply the reference keeps
-            // (kernels/elementwise.py:53-56).
-            o[2 * j] = __builtin_fmaf(xr, c[j], -(xi * s[j]));
-            o[2 * j + 1] = __builtin_fmaf(xi, c[j], xr * s[j]);
-        }
-        return pack8(o);
-    } else {
-        return pack8(x);
-    }
+    if constexpr (ROPE) head_rope8(x, f0, f1);
+    return pack8(x);
 }
 
 // q/k: (B, S, H, D) -> oq (B, S, H, D), ok (B, P+S, H, D); v -> ov at the

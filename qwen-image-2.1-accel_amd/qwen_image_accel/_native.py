@@ -17,7 +17,7 @@ LIB_PATH = os.environ.get("QIM_LIBRARY", os.path.join(os.path.dirname(os.path.ab
 QIM_OK, QIM_ERR_ARG, QIM_ERR_SHAPE, QIM_ERR_LAYOUT, QIM_ERR_LAUNCH = range(5)
 ADALN_ADD_ONE, ADALN_TILED = 1, 2
 GEMM_A_TILED, GEMM_B_TILED, GEMM_OUT_TILED = 1, 2, 4
-EPI_NONE, EPI_BIAS, EPI_GATED_RESIDUAL, EPI_SWIGLU, EPI_SWIGLU_QUANT = range(5)
+EPI_NONE, EPI_BIAS, EPI_GATED_RESIDUAL, EPI_SWIGLU, EPI_SWIGLU_QUANT, EPI_QK_NORM_ROPE = range(6)
 SWIGLU_GROUP = 32
 
 
@@ -58,6 +58,7 @@ SIGNATURES = {
     "qim_qk_norm_rope_pack": (_C, [_P] * 11 + [_I] * 6 + [_F, _F, _P]),
     "qim_mxfp8_gemm": (_C, [_P, _P, _P, _P, _I, _I, _I, _C, _P, _P, _P, _I, _P, _I, _P, _P]),
     "qim_mxfp8_gemm_ex": (_C, [_P, _P, _P, _P, _I, _I, _I, _C, _C, _P, _P, _P, _I, _P, _I, _P, _P]),
+    "qim_mxfp8_gemm_qk_norm_rope": (_C, [_P, _P, _P, _P, _I, _I, _I, _C, _P, _P, _P, _I, _F, _F, _P, _I, _P]),
     "qim_debug_e4m3_encode": (_C, [_P, _P, _I, _P]),
     "qim_debug_bf16_round": (_C, [_P, _P, _I, _P]),
     "qim_debug_mfma_tile": (_C, [_P, _P, _P, _P, _P, _P]),

@@ -7,15 +7,16 @@ eager definition WHL!diffusers/models/transformers/transformer_qwenimage21.py:
 modulation, fused QKV projection, hidden 3072, 24 heads x 128, FFN 12288):
 
     x   = MXFP8(LN(h) * (1 + scale1) + shift1)             qim_adaln_quantize
-    qkv = x @ W_qkv                                         qim_mxfp8_gemm
-    q,k = rope(RMSNorm(q)), rope(RMSNorm(k))                qim_qk_norm_rope_pack
+    qkv = x @ W_qkv; q,k = rope(RMSNorm(q)), rope(RMSNorm(k))
+                                                            qim_mxfp8_gemm_qk_norm_rope
     o   = attention(q, k, v)        -- out of scope; stand-in o = v
     h   = h + tanh(g1) * (MXFP8(o) @ W_out)                 qim_mx_quantize + GEMM epilogue
     x   = MXFP8(LN(h) * (1 + scale2) + shift2)             qim_adaln_quantize
     a   = MXFP8(silu(x @ W_gate) * (x @ W_up))              GEMM, SwiGLU->MXFP8 epilogue
     h   = h + tanh(g2) * (a @ W_down)                       GEMM, gated-residual epilogue
 
-Eight launches; every MXFP8 operand (weights and activations) is in the GEMM's
+Seven launches (QK-RMSNorm + RoPE run in the QKV GEMM's epilogue, head by
+head: each wave of the GEMM holds whole 128-wide head rows); every MXFP8 operand (weights and activations) is in the GEMM's
 tiled code layout, written that way by its producer; every bf16 rounding point
 of the eager block is kept (the
 activation quantizations share one FP8 tensor per consumer group, as in
@@ -27,7 +28,7 @@ from dataclasses import dataclass
 
 import torch
 
-from qwen_image_accel.kernels import attention, gemm, mxfp8
+from qwen_image_accel.kernels import gemm, mxfp8
 from qwen_image_accel.kernels.epilogue import layer_norm_scale_quantize
 
 
@@ -93,11 +94,11 @@ class MMDiTBlock:
 
         x = layer_norm_scale_quantize(h, scale1.contiguous(), norm, shift=shift1.contiguous(),
                                       add_one=True, tiled=True)
-        qkv = self._mm(x, self.w_qkv)                                            # (B*S, 3d)
+        qkv = gemm.mx_matmul_qk_norm_rope(x, self.w_qkv.values, self.w_qkv.scales, self.norm_q, self.norm_k,
+                                          freqs, self.heads, s, self.eps, self.eps, weight_tiled=True)
         qkv4 = qkv.view(b, s, 3 * d)
-        q = qkv4[:, :, :d].unflatten(-1, (self.heads, hd))
+        q = qkv4[:, :, :d].unflatten(-1, (self.heads, hd))                      # normalised + rotated
         k = qkv4[:, :, d:2 * d].unflatten(-1, (self.heads, hd))
-        q, k = attention.qk_norm_rope(q, k, self.norm_q, self.norm_k, freqs, self.eps, self.eps)
         if attention_fn is None:
             o = qkv[:, 2 * d:]                                                   # stand-in: v
         else:

@@ -21,6 +21,37 @@ EPILOGUES = {
 }
 
 
+def mx_matmul_qk_norm_rope(activation, weight_fp8, weight_scale, weight_q, weight_k, freqs, heads, seq,
+                           eps_q=1e-6, eps_k=1e-6, *, weight_tiled=False, out=None):
+    """The MMDiT block's QKV projection with QK-RMSNorm + RoPE in its epilogue.
+
+    Returns the bf16 ``(rows, 3 * heads * 128)`` projection whose Q and K
+    columns are ``rope(RMSNorm(.))`` per 128-wide head -- what
+    ``kernels.attention.qk_norm_rope`` computes on the unfused output -- and
+    whose V columns are the plain product.  ``freqs``: complex64 (seq, 64),
+    row = output row % seq.  No reference counterpart as one call: it fuses
+    kernels/attention.py:16-89 into optimizations/mxfp8.py:32-36."""
+    a = activation
+    w = weight_fp8 if weight_tiled else weight_rows(weight_fp8)
+    n, k = w.shape
+    if n != 3 * heads * 128 or a.values.shape[1] != k:
+        raise ValueError(f"QKV weight must be (3 * {heads} * 128, K) with the activation's K")
+    if freqs.dtype != torch.complex64 or freqs.shape != (seq, 64):
+        raise ValueError("freqs must be complex64 (seq, 64)")
+    m = a.rows
+    if out is None:
+        out = torch.empty((m, n), device=a.values.device, dtype=torch.bfloat16)
+    if out.dtype != torch.bfloat16 or out.stride(-1) != 1 or out.shape != (m, n):
+        raise ValueError("out must be a bf16 (rows, N) tensor with unit column stride")
+    layouts = (_native.GEMM_A_TILED if a.tiled else 0) | (_native.GEMM_B_TILED if weight_tiled else 0)
+    f = torch.view_as_real(freqs.contiguous())
+    _native.call("qim_mxfp8_gemm_qk_norm_rope", _native.ptr(a.values), _native.ptr(a.scales), _native.ptr(w),
+                 _native.ptr(weight_scale), m, k, heads, layouts, _native.ptr(weight_q), _native.ptr(weight_k),
+                 _native.ptr(f), seq, float(eps_q), float(eps_k), _native.ptr(out), out.stride(0),
+                 _native.stream(out.device))
+    return out
+
+
 def weight_rows(weight_fp8):
     """The (N, K) row-major code matrix behind a weight given either as the
     reference's column-major (K, N) ``values.t()`` view or as (N, K)."""
