@@ -372,9 +372,12 @@ def main():
                      ("block_1024", lambda: bench_block(4352, steps, warm)),
                      ("block_2048", lambda: bench_block(16640, steps, warm)),
                      ("copy_256MiB", lambda: bench_copy(steps, warm)),
-                     # copies moving the algorithmic bytes of configs 1 and 2
+                     # copies moving the algorithmic bytes of each bandwidth-bound config
                      ("copy_23.6MB", lambda: bench_copy(steps, warm, 23611392 // 2, "23.6 MB moved")),
-                     ("copy_109MB", lambda: bench_copy(steps, warm, 109183488 // 2, "109.2 MB moved"))]:
+                     ("copy_40.5MB", lambda: bench_copy(steps, warm, 40525824 // 2, "40.5 MB moved")),
+                     ("copy_80.2MB", lambda: bench_copy(steps, warm, 80222208 // 2, "80.2 MB moved")),
+                     ("copy_109MB", lambda: bench_copy(steps, warm, 109183488 // 2, "109.2 MB moved")),
+                     ("copy_320.9MB", lambda: bench_copy(steps, warm, 320864256 // 2, "320.9 MB moved"))]:
         if not want(name):
             continue
         log(f"[bench] {name} ...")
@@ -406,11 +409,18 @@ def main():
                            "kernel": head["kernel"], "algorithmic_bytes": head["bytes"],
                            "traffic_source": "profiles/traffic.json: rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE per "
                                              "dispatch, each scaled by its reading for a 256 MiB copy"}
+    # Each bandwidth-bound op against a copy moving the same bytes in one launch.
+    same_size_copy = {"adaln_512": "copy_23.6MB", "quantize_1024": "copy_40.5MB",
+                      "gated_residual_1024": "copy_80.2MB", "qk_norm_rope_1024": "copy_109MB",
+                      "swiglu_1024": "copy_320.9MB"}
     summary = {}
     for k, v in comp.items():
         e = {"us": round(v["us"], 2)}
         if "gbs" in v:
             e.update(GBs=round(v["gbs"], 1), hbm_frac=round(v["frac"], 4))
+            ref = comp.get(same_size_copy.get(k, ""))
+            if ref:
+                e["of_same_size_copy"] = round(ref["us"] / v["us"], 4)
         if "tflops" in v:
             e.update(TFLOPs=round(v["tflops"], 1), mfma_frac=round(v.get("frac", v.get("gemm_frac")), 4))
         summary[k] = e
