@@ -48,6 +48,33 @@ def prepare_attention_inputs(q, k, v, norm_q, norm_k, freqs, cached_k, cached_v)
     return oq, ok, ov
 
 
+def attention(q, k, v, scale=None, out=None):
+    """softmax(q k^T * scale) v per (batch, head): libqim's ``qim_attention``.
+
+    q: (B, S, H, 128), k, v: (B, T, H, 128) bf16 on the GPU, each with unit
+    stride inside a token and any token stride (e.g. views into a fused QKV
+    projection).  scale defaults to 1/sqrt(128).  Returns (B, S, H, 128) bf16.
+    The block's attention core; the reference calls torch SDPA there
+    (optimizations/quantized_decode.py:70-77)."""
+    b, s, h, d = q.shape
+    t = k.shape[1]
+    for x, n in ((q, s), (k, t), (v, t)):
+        if (x.dtype != torch.bfloat16 or not x.is_cuda or x.shape != (b, n, h, d) or x.stride(3) != 1
+                or x.stride(2) != d or x.stride(0) != n * x.stride(1)):
+            raise _native.Unsupported("attention", _native.QIM_ERR_LAYOUT,
+                                      "expects bf16 (B, N, H, D) tensors with packed heads and token rows")
+    if out is None:
+        out = torch.empty((b, s, h, d), device=q.device, dtype=torch.bfloat16)
+    nbytes = _native.lib().qim_attention_workspace_bytes(b, t, h, d)
+    if nbytes <= 0:
+        raise _native.Unsupported("attention", _native.QIM_ERR_SHAPE, f"head dim {d} (128 only)")
+    ws = torch.empty(nbytes // 2, device=q.device, dtype=torch.bfloat16)
+    _native.call("qim_attention", _native.ptr(q), q.stride(1), _native.ptr(k), k.stride(1), _native.ptr(v),
+                 v.stride(1), _native.ptr(out), out.stride(1), _native.ptr(ws), b, s, t, h, d,
+                 float(scale if scale is not None else d ** -0.5), _native.stream(q.device))
+    return out
+
+
 def qk_norm_rope(q, k, weight_q, weight_k, freqs, eps_q=1e-6, eps_k=1e-6, heads=None):
     """Fused QK-RMSNorm + RoPE without a V pack (the MMDiT block's form).
 

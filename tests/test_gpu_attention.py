@@ -1,0 +1,69 @@
+"""The attention core (qim_attention) against softmax(Q K^T * scale) V in
+float32 on the CPU, on the same bf16 inputs.
+
+Bar: the kernel rounds P to bf16 for the P V product and writes bf16, so the
+output is held to rel-Frobenius <= 1e-2 and a max-abs error of 2 % of the
+output's largest magnitude, like the GEMM.  Shapes cover ragged query and key
+counts (the last 256-query and 64-key blocks partial), two batches with a
+cached prefix (T = P + S), Q/K/V as strided views into one fused QKV output,
+and large logits (the running-max subtraction).
+"""
+import pytest
+import torch
+
+from qwen_image_accel.kernels import attention
+from tests.helpers import bf16_randn, rel_fro
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+def reference(q, k, v, scale):
+    """(B, S, H, D) bf16 -> float32 softmax attention, computed on the CPU."""
+    qf, kf, vf = (x.float().cpu().permute(0, 2, 1, 3) for x in (q, k, v))  # (B, H, N, D)
+    w = torch.softmax(torch.matmul(qf, kf.transpose(-1, -2).contiguous()) * scale, dim=-1)
+    return torch.matmul(w, vf).permute(0, 2, 1, 3)
+
+
+def check(out, ref):
+    got = out.float().cpu()
+    err = rel_fro(got.numpy(), ref.numpy())
+    mx = (got - ref).abs().max().item()
+    assert err < 1e-2, err
+    assert mx < 0.02 * ref.abs().max().item(), mx
+
+
+@pytest.mark.parametrize("b,s,t,h,mag", [(1, 300, 300, 2, 1.0), (2, 256, 333, 3, 1.0), (1, 64, 1000, 1, 1.0),
+                                         (1, 520, 520, 2, 8.0)])
+def test_attention_packed(dev, b, s, t, h, mag):
+    say("attention", b, s, t, h, mag)
+    g = torch.Generator().manual_seed(b * 1000 + s + t + h)
+    q = (bf16_randn(g, (b, s, h, 128)) * mag).to(torch.bfloat16).to(dev)
+    k = bf16_randn(g, (b, t, h, 128)).to(dev)
+    v = bf16_randn(g, (b, t, h, 128)).to(dev)
+    scale = 128 ** -0.5
+    out = attention.attention(q, k, v)
+    torch.cuda.synchronize()
+    check(out, reference(q, k, v, scale))
+
+
+def test_attention_on_fused_qkv_views(dev):
+    """Q, K, V as column blocks of one (B, S, 3HD) projection (token stride 3HD)."""
+    b, s, h = 1, 384, 4
+    say("attention qkv views", b, s, h)
+    g = torch.Generator().manual_seed(5)
+    qkv = bf16_randn(g, (b, s, 3 * h * 128)).to(dev)
+    q, k, v = (qkv[:, :, i * h * 128:(i + 1) * h * 128].unflatten(-1, (h, 128)) for i in range(3))
+    out = attention.attention(q, k, v, scale=0.1)
+    torch.cuda.synchronize()
+    check(out, reference(q, k, v, 0.1))
+
+
+def test_attention_rejects_other_head_dims(dev):
+    from qwen_image_accel import _native
+    x = torch.zeros(1, 8, 1, 64, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(_native.Unsupported):
+        attention.attention(x, x, x)
