@@ -32,9 +32,18 @@ COMMON = [
 ]
 
 
+# Per-source additions.  qim_attention.hip: MFMA accumulators in architectural
+#   VGPRs (the "VGPR form"), operands in AGPRs, so the softmax reads the score
+#   tiles and the lazy O rescale multiplies O in place; the accumulation-
+#   register form copies every tile through v_accvgpr_read/write instead.
+EXTRA = {
+    "qim_attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile(src):
     obj = os.path.join(BUILD, os.path.basename(src).replace(".hip", ".o"))
-    cmd = [HIPCC, *COMMON, "-c", src, "-o", obj]
+    cmd = [HIPCC, *COMMON, *EXTRA.get(os.path.basename(src), []), "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     msgs = "\n".join(l for l in (r.stdout + r.stderr).splitlines()
                      if "packed-fp32-ops" not in l)

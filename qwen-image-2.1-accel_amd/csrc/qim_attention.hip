@@ -36,8 +36,8 @@ constexpr int ATT_KB = 64;          // keys per block
 constexpr int ATT_BQ = 256;         // queries per workgroup: 4 waves x 2 tiles of 32
 constexpr int ATT_TILE = ATT_KB * ATT_D * 2;  // 16 KiB: one K block or one V^T block
 constexpr int ATT_STAGE = 2 * ATT_TILE;       // K + V^T
-constexpr int ATT_NSTAGE = 3;
-constexpr int ATT_LDS = ATT_NSTAGE * ATT_STAGE;  // 96 KiB
+constexpr int ATT_NSTAGE = 4;
+constexpr int ATT_LDS = ATT_NSTAGE * ATT_STAGE;  // 128 KiB
 
 struct AttnArgs {
     const uint16_t *q, *k;
@@ -102,7 +102,6 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(const uint4 &u) { return __builtin
 // is clamped by the caller.  K instruction n covers keys 4n..4n+3: lane i
 // lands at LDS row key 4n + i/16, physical chunk i % 16, whose source is the
 // key's logical chunk (i % 16) ^ (key & 15).  V^T tiles are copied as they are.
-
 __device__ __forceinline__ void att_issue(const AttnArgs &p, int b, int h, int wave, int lane, uint8_t *slot, int kb) {
     const uint32_t base = att_lds_addr(slot);
 #pragma unroll
@@ -123,13 +122,160 @@ __device__ __forceinline__ void att_issue(const AttnArgs &p, int b, int h, int w
     }
 }
 
+// K fragments of one 32-key sub-block (half hb of an LDS key block), all 8
+// head-dim steps: lane (r = key % 32, hf) reads d [16j + 8hf, +8) of key r.
+__device__ __forceinline__ void att_read_k(uint4 (&kf)[8], const uint8_t *kt_lds, int hb, int lq, int hf) {
+    const int r = 32 * hb + lq;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        kf[j] = *reinterpret_cast<const uint4 *>(kt_lds + r * 256 + (((2 * j + hf) ^ (r & 15)) * 16));
+}
+
+// V^T fragments of one 32-key sub-block: lane (d % 32, hf) reads the 8 keys of
+// 16-key step kk = 2hb + u that pair with its P^T operand, head dims 32dt + d % 32.
+__device__ __forceinline__ void att_read_v(uint4 (&vf)[2][4], const uint8_t *vt_lds, int hb, int lq, int hf) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+            const int d = 32 * dt + lq, kk = 2 * hb + u;
+            vf[u][dt] = *reinterpret_cast<const uint4 *>(vt_lds + d * (ATT_KB * 2) + (((2 * kk + hf) ^ ((d >> 1) & 7)) * 16));
+        }
+}
+
+// S^T of one 32-query tile over one 32-key sub-block: 8 MFMAs.
+__device__ __forceinline__ void att_scores(f32x16a_t &s, const uint4 (&kf)[8], const uint4 (&qf)[8]) {
+    s = f32x16a_t{};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(kf[j]), as_bf16x8(qf[j]), s, 0, 0, 0);
+}
+
+// O^T += V^T P^T for one 32-query tile over one 32-key sub-block: 8 MFMAs.
+__device__ __forceinline__ void att_pv(f32x16a_t (&o)[4], const uint4 (&vf)[2][4], const uint4 (&pf)[2]) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+            o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(vf[u][dt]), as_bf16x8(pf[u]), o[dt], 0, 0, 0);
+}
+
+// Keys at or past T (the partial last sub-block) get a score of -inf.
+__device__ __forceinline__ void att_mask(f32x16a_t &s, int kbase, int T, int hf) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int key = kbase + 8 * (i >> 2) + 4 * hf + (i & 3);
+        if (key >= T) s[i] = -__builtin_inff();
+    }
+}
+
+// Scores above the running reference max m by at most ATT_RESCALE (log2
+// units) are exponentiated against m as they are: P <= 2^ATT_RESCALE, which
+// bf16 P and the fp32 sums hold as well as P <= 1.  Only a sub-block whose max
+// exceeds that moves m (to the sub-block max) and rescales O and l.
+constexpr float ATT_RESCALE = 8.0f;
+
+__device__ __forceinline__ float att_max(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
+// Online softmax of one 32-query tile over one 32-key sub-block.  In: the raw
+// scores s (this lane's 16 keys of query lq; the other half-wave holds the
+// other 16).  Updates the scaled reference max m and the partial sum l (this
+// lane's keys; the half-waves' sums are added at the end), writes P as the
+// bf16 B operands of the P V product and returns the factor O must be
+// multiplied by before this sub-block's P V.
+__device__ __forceinline__ float att_softmax(const f32x16a_t &s, float &m, float &l, uint4 (&pf)[2], float c) {
+    float a0 = att_max(s[0], s[1]), a1 = att_max(s[2], s[3]);
+#pragma unroll
+    for (int i = 4; i < 16; i += 4) {
+        a0 = att_max(a0, att_max(s[i], s[i + 1]));
+        a1 = att_max(a1, att_max(s[i + 2], s[i + 3]));
+    }
+    const float mx0 = att_max(a0, a1);
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx0), __float_as_uint(mx0), false, false);
+    const float mx = att_max(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * c;
+    const float mnew = mx > m + ATT_RESCALE ? mx : m;
+    const float alpha = __builtin_amdgcn_exp2f(m - mnew);  // 1 if m stays, 0 on the first sub-block
+    m = mnew;
+    const bf16x2_t ones = {(__bf16)1.0f, (__bf16)1.0f};
+    float sum0 = 0.f, sum1 = 0.f;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * u + 2 * e], c, -mnew));
+            const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * u + 2 * e + 1], c, -mnew));
+            w[e] = pack_bf16x2(p0, p1);
+        }
+        pf[u] = make_uint4(w[0], w[1], w[2], w[3]);
+        // l sums the bf16 P that the P V product uses.
+        sum0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w[0]), ones, sum0, false);
+        sum1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w[1]), ones, sum1, false);
+        sum0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w[2]), ones, sum0, false);
+        sum1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w[3]), ones, sum1, false);
+    }
+    l = l * alpha + (sum0 + sum1);
+    // Pin the whole softmax before the rescale branch that follows it, inside
+    // the region whose MFMAs it runs beside (else the compiler sinks the
+    // exponentials past the branch, after those MFMAs).
+    u32x4_t v0 = {pf[0].x, pf[0].y, pf[0].z, pf[0].w}, v1 = {pf[1].x, pf[1].y, pf[1].z, pf[1].w};
+    asm volatile("" : "+v"(v0), "+v"(v1), "+v"(l));
+    pf[0] = make_uint4(v0.x, v0.y, v0.z, v0.w);
+    pf[1] = make_uint4(v1.x, v1.y, v1.z, v1.w);
+    return alpha;
+}
+
+// o *= alpha, skipped (wave-uniform) when no query of the wave moved its max.
+__device__ __forceinline__ void att_rescale(f32x16a_t (&o)[4], float alpha) {
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+    }
+}
+
+// Instruction interleave of one region: N MFMAs, each followed by up to V
+// vector-ALU (incl. transcendental) and R LDS-read instructions.
+template <int N, int V, int R>
+__device__ __forceinline__ void att_interleave() {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (R > 0) __builtin_amdgcn_sched_group_barrier(0x100, R, 0);
+        __builtin_amdgcn_sched_group_barrier(0x402, V, 0);
+    }
+}
+
+// Per wave: 64 queries in two 32-query tiles (0, 1), keys in 32-key
+// sub-blocks u (two per 64-key LDS block).  Per sub-block the work is S_t =
+// K Q_t^T, the softmax SM_t and O_t += V^T P_t^T; it runs software-pipelined
+// in two steps so that each softmax runs on the vector ALU beside 16 MFMAs
+// that do not depend on it:
+//   X(u): MFMA S_1(u), PV_1(u-1)   | VALU SM_0(u) | LDS reads of V^T(u), K(u+1)
+//   Y(u): MFMA PV_0(u), S_0(u+1)   | VALU SM_1(u)
+// Every K and V^T fragment is read from LDS once and used for both query
+// tiles; the fragments alternate between two register sets by the parity of u.
+// LDS holds four 64-key blocks: block n + 2 is issued into the slot of block
+// n - 2 at the barrier before X(2n - 1), after the last read of that slot.
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_attn_fwd(AttnArgs p) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int qblk = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int lq = lane & 31, hf = lane >> 5;
-    const int q0 = qblk * ATT_BQ + wave * 64;  // this wave's 64 queries: tiles t = 0, 1 of 32
+
+    // XCD-aware order: consecutive workgroup ids go to different XCDs
+    // (round-robin over 8); remap so that each XCD runs a contiguous range of
+    // (query block, head, batch) work items, i.e. the query blocks of few
+    // heads at a time, which share K and V^T in that XCD's L2.
+    int qblk, h, b;
+    {
+        const int nq = gridDim.x, nw = gridDim.x * gridDim.y * gridDim.z;
+        const int lin = blockIdx.x + nq * (blockIdx.y + gridDim.y * blockIdx.z);
+        const int xcd = lin & 7, base = nw >> 3, rem = nw & 7;
+        const int w = xcd * base + (xcd < rem ? xcd : rem) + (lin >> 3);
+        qblk = w % nq;
+        h = (w / nq) % gridDim.y;
+        b = w / (nq * gridDim.y);
+    }
+    const int q0 = qblk * ATT_BQ + wave * 64;
 
     // Q^T operands: lane (q, hf) holds d [16j + 8hf, +8) of query q0 + 32t + q.
     uint4 qf[2][8];
@@ -141,114 +287,128 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
         for (int j = 0; j < 8; ++j) qf[t][j] = *reinterpret_cast<const uint4 *>(qrow + 16 * j);
     }
-
-    att_issue(p, b, h, wave, lane, lds, 0);
-    att_issue(p, b, h, wave, lane, lds + ATT_STAGE, 1 < p.nkb ? 1 : p.nkb - 1);
-
-    f32x16a_t o[2][4];
+    // Q^T is only ever an MFMA operand: keep it in accumulation registers, which
+    // leaves the architectural ones to the K / V^T fragments, P and the softmax.
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt) o[t][dt] = f32x16a_t{};
-    float m[2] = {-__builtin_inff(), -__builtin_inff()}, l[2] = {0.f, 0.f};
+        for (int j = 0; j < 8; ++j) {
+            u32x4_t v = {qf[t][j].x, qf[t][j].y, qf[t][j].z, qf[t][j].w};
+            asm volatile("" : "+a"(v));
+            qf[t][j] = make_uint4(v.x, v.y, v.z, v.w);
+        }
 
-    for (int kb = 0; kb < p.nkb; ++kb) {
-        // Block kb landed (block kb + 1 may still be in flight) for every wave,
-        // and every wave is done with block kb - 1, whose slot is reloaded next.
-        // A bare s_barrier: __syncthreads would also drain the loads in flight.
+    const int nkb = p.nkb, lastb = nkb - 1;
+    // Keys past T exist only in the last block; a sub-block there may be all
+    // masked, which gives P = 0 and leaves m, l and O as they are.
+    const bool ragged = (p.T & (ATT_KB - 1)) != 0;
+    const float c = p.scale_log2e;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) att_issue(p, b, h, wave, lane, lds + i * ATT_STAGE, i < nkb ? i : lastb);
+
+    f32x16a_t o0[4], o1[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) o0[dt] = o1[dt] = f32x16a_t{};
+    float m0 = -__builtin_inff(), m1 = -__builtin_inff(), l0 = 0.f, l1 = 0.f;
+    uint4 kfa[8], kfb[8], vfa[2][4], vfb[2][4], pf0[2], pf1[2];
+    f32x16a_t s0, s1;
+    auto slot = [&](int n) { return lds + (n & 3) * ATT_STAGE; };
+
+    // Prologue: block 0 landed for every wave; S_0(0); X(0) without a P V.
+    att_wait_vmcnt<16>();
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    att_read_k(kfa, lds, 0, lq, hf);
+    att_scores(s0, kfa, qf[0]);
+    if (lastb == 0 && ragged) att_mask(s0, 0, p.T, hf);
+    {
+        att_scores(s1, kfa, qf[1]);
+        const float alpha = att_softmax(s0, m0, l0, pf0, c);
+        att_read_v(vfa, slot(0) + ATT_TILE, 0, lq, hf);
+        att_read_k(kfb, slot(0), 1, lq, hf);
+        att_interleave<8, 8, 2>();
+        att_rescale(o0, alpha);
+    }
+    // Block n: sub-blocks u = 2n (fragments in the "a" registers) and 2n + 1 ("b").
+    for (int n = 0; n < lastb; ++n) {
+        const bool mask_next = n + 1 == lastb && ragged;
+        // ---- Y(2n): P V with vfa, next scores with kfb
+        {
+            att_pv(o0, vfa, pf0);
+            att_scores(s0, kfb, qf[0]);
+            const float alpha = att_softmax(s1, m1, l1, pf1, c);
+            att_interleave<16, 4, 0>();
+            att_rescale(o1, alpha);
+        }
+        // Block n + 1 (K of sub-block 2n + 2, read in X(2n + 1)) landed for
+        // every wave; the slot of block n - 1 is free: issue block n + 3 there.
         att_wait_vmcnt<8>();
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        att_issue(p, b, h, wave, lane, slot(n + 3), n + 3 < nkb ? n + 3 : lastb);
+        // ---- X(2n + 1): scores with kfb, P V with vfa; reads vfb, kfa
         {
-            const int nb = kb + 2 < p.nkb ? kb + 2 : p.nkb - 1;
-            att_issue(p, b, h, wave, lane, lds + ((kb + 2) % ATT_NSTAGE) * ATT_STAGE, nb);
+            att_scores(s1, kfb, qf[1]);
+            att_pv(o1, vfa, pf1);
+            const float alpha = att_softmax(s0, m0, l0, pf0, c);
+            att_read_v(vfb, slot(n) + ATT_TILE, 1, lq, hf);
+            att_read_k(kfa, slot(n + 1), 0, lq, hf);
+            att_interleave<16, 4, 1>();
+            att_rescale(o0, alpha);
         }
-        const uint8_t *kt_lds = lds + (kb % ATT_NSTAGE) * ATT_STAGE;
-        const uint8_t *vt_lds = kt_lds + ATT_TILE;
-
-        // S^T = K Q^T: two 32-key tiles x two 32-query tiles, 8 steps of 16 d.
-        f32x16a_t s[2][2];
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt) s[t][kt] = f32x16a_t{};
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt) {
-                const int r = 32 * kt + lq;
-                const int pc = (2 * j + hf) ^ (r & 15);
-                const uint4 kf = *reinterpret_cast<const uint4 *>(kt_lds + r * 256 + pc * 16);
-#pragma unroll
-                for (int t = 0; t < 2; ++t)
-                    s[t][kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(kf), as_bf16x8(qf[t][j]), s[t][kt],
-                                                                       0, 0, 0);
-            }
+        // ---- Y(2n + 1): P V with vfb, next scores with kfa
+        {
+            att_pv(o0, vfb, pf0);
+            att_scores(s0, kfa, qf[0]);
+            const float alpha = att_softmax(s1, m1, l1, pf1, c);
+            att_interleave<16, 4, 0>();
+            att_rescale(o1, alpha);
         }
-
-        // Online softmax per query (lane-local over this lane's 32 keys, plus
-        // the other half-wave's 32 keys of the same query).
-        const int kbase = kb * ATT_KB;
-        uint4 pf[2][2][2];  // bf16 P^T operands [query tile][key tile][16-key step]
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            float x[2][16];
-            float mx = -__builtin_inff();
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int key = kbase + 32 * kt + 8 * (i >> 2) + 4 * hf + (i & 3);
-                    x[kt][i] = key < p.T ? s[t][kt][i] * p.scale_log2e : -__builtin_inff();
-                    mx = x[kt][i] > mx ? x[kt][i] : mx;
-                }
-            const float mo = __shfl_xor(mx, 32, 64);
-            mx = mo > mx ? mo : mx;
-            const float mnew = m[t] > mx ? m[t] : mx;
-            const float alpha = mnew == -__builtin_inff() ? 1.0f : __builtin_amdgcn_exp2f(m[t] - mnew);
-            float sum = 0.f;
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const float e = mnew == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(x[kt][i] - mnew);
-                    x[kt][i] = e;
-                    sum += e;
-                }
-            l[t] = l[t] * alpha + sum;
-            m[t] = mnew;
-#pragma unroll
-            for (int dt = 0; dt < 4; ++dt) o[t][dt] *= alpha;
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                for (int u = 0; u < 2; ++u)
-                    pf[t][kt][u] = make_uint4(pack_bf16x2(x[kt][8 * u + 0], x[kt][8 * u + 1]),
-                                              pack_bf16x2(x[kt][8 * u + 2], x[kt][8 * u + 3]),
-                                              pack_bf16x2(x[kt][8 * u + 4], x[kt][8 * u + 5]),
-                                              pack_bf16x2(x[kt][8 * u + 6], x[kt][8 * u + 7]));
-        }
-
-        // O^T += V^T P^T: four 32-dim tiles, four 16-key steps.
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-#pragma unroll
-            for (int dt = 0; dt < 4; ++dt) {
-                const int d = 32 * dt + lq;
-                const int pc = (2 * kk + hf) ^ ((d >> 1) & 7);
-                const uint4 vf = *reinterpret_cast<const uint4 *>(vt_lds + d * (ATT_KB * 2) + pc * 16);
-#pragma unroll
-                for (int t = 0; t < 2; ++t)
-                    o[t][dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(vf), as_bf16x8(pf[t][kk >> 1][kk & 1]),
-                                                                       o[t][dt], 0, 0, 0);
-            }
+        if (mask_next) att_mask(s0, (n + 1) * ATT_KB, p.T, hf);
+        // ---- X(2n + 2): scores with kfa, P V with vfb; reads vfa, kfb
+        {
+            att_scores(s1, kfa, qf[1]);
+            att_pv(o1, vfb, pf1);
+            const float alpha = att_softmax(s0, m0, l0, pf0, c);
+            att_read_v(vfa, slot(n + 1) + ATT_TILE, 0, lq, hf);
+            att_read_k(kfb, slot(n + 1), 1, lq, hf);
+            att_interleave<16, 4, 1>();
+            att_rescale(o0, alpha);
         }
     }
+    // Last block: Y(2L), X(2L + 1), Y(2L + 1) and PV_1(2L + 1); its data landed
+    // at the last barrier (or the prologue's), no further loads.
+    if (ragged) att_mask(s1, lastb * ATT_KB, p.T, hf);
+    {
+        att_pv(o0, vfa, pf0);
+        att_scores(s0, kfb, qf[0]);
+        const float alpha = att_softmax(s1, m1, l1, pf1, c);
+        att_interleave<16, 4, 0>();
+        att_rescale(o1, alpha);
+    }
+    if (ragged) att_mask(s0, lastb * ATT_KB + 32, p.T, hf);
+    {
+        att_scores(s1, kfb, qf[1]);
+        att_pv(o1, vfa, pf1);
+        const float alpha = att_softmax(s0, m0, l0, pf0, c);
+        att_read_v(vfb, slot(lastb) + ATT_TILE, 1, lq, hf);
+        att_interleave<16, 4, 1>();
+        att_rescale(o0, alpha);
+    }
+    if (ragged) att_mask(s1, lastb * ATT_KB + 32, p.T, hf);
+    {
+        att_pv(o0, vfb, pf0);
+        const float alpha = att_softmax(s1, m1, l1, pf1, c);
+        att_interleave<8, 8, 0>();
+        att_rescale(o1, alpha);
+    }
+    att_pv(o1, vfb, pf1);
     att_wait_vmcnt<0>();  // the clamped tail loads land before the workgroup ends
 
     // O = O^T / l: lane (q, hf) holds dims 32dt + 8(i/4) + 4hf + i%4 of its query.
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-        const float lt = l[t] + __shfl_xor(l[t], 32, 64);
+        const f32x16a_t(&o)[4] = t ? o1 : o0;
+        const float lf = t ? l1 : l0;
+        const float lt = lf + __shfl_xor(lf, 32, 64);
         const float inv = 1.0f / lt;
         const int qi = q0 + 32 * t + lq;
         if (qi >= p.S) continue;
@@ -258,8 +418,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int d = 32 * dt + 8 * g + 4 * hf;
-                const uint2 w = make_uint2(pack_bf16x2(o[t][dt][4 * g + 0] * inv, o[t][dt][4 * g + 1] * inv),
-                                           pack_bf16x2(o[t][dt][4 * g + 2] * inv, o[t][dt][4 * g + 3] * inv));
+                const uint2 w = make_uint2(pack_bf16x2(o[dt][4 * g + 0] * inv, o[dt][4 * g + 1] * inv),
+                                           pack_bf16x2(o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv));
                 *reinterpret_cast<uint2 *>(orow + d) = w;
             }
     }
@@ -274,6 +434,7 @@ extern "C" int qim_attention(const void *q, int64_t ldq, const void *k, int64_t 
                              int64_t D, float scale, void *stream) {
     QIM_REQUIRE(q && k && v && o && vt_workspace, QIM_ERR_ARG, "qim_attention: null pointer");
     QIM_REQUIRE(D == ATT_D, QIM_ERR_SHAPE, "qim_attention: head dim %lld (128 only)", (long long)D);
+    QIM_REQUIRE(scale > 0.0f && scale < 1e30f, QIM_ERR_ARG, "qim_attention: scale must be positive and finite");
     QIM_REQUIRE(B > 0 && S > 0 && T > 0 && H > 0, QIM_ERR_SHAPE, "qim_attention: empty problem");
     QIM_REQUIRE(B < 65536 && H < 65536 && S < (1 << 30) && T < (1 << 30), QIM_ERR_SHAPE, "qim_attention: too large");
     QIM_REQUIRE(ldq >= H * D && ldk >= H * D && ldv >= H * D && ldo >= H * D && ldq % 8 == 0 && ldk % 8 == 0 &&
