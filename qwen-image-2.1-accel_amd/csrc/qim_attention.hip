@@ -98,28 +98,55 @@ __device__ __forceinline__ void att_wait_vmcnt() {
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(const uint4 &u) { return __builtin_bit_cast(bf16x8_t, u); }
 
-// The 8 DMA instructions of one wave for key block kb (4 of K, 4 of V^T); kb
-// is clamped by the caller.  K instruction n covers keys 4n..4n+3: lane i
-// lands at LDS row key 4n + i/16, physical chunk i % 16, whose source is the
-// key's logical chunk (i % 16) ^ (key & 15).  V^T tiles are copied as they are.
-__device__ __forceinline__ void att_issue(const AttnArgs &p, int b, int h, int wave, int lane, uint8_t *slot, int kb) {
-    const uint32_t base = att_lds_addr(slot);
+// DMA addressing of one wave's share of a key block: 4 instructions of K and
+// 4 of V^T (1 KiB each).  K instruction j (n = 4 wave + j) covers keys
+// 4n..4n+3 of the block: lane i lands at LDS row r = 4n + i/16, physical chunk
+// i % 16, whose source is the key's logical chunk (i % 16) ^ (r & 15).  Per
+// block only the (wave-uniform) base address moves; the per-lane offsets are
+// fixed, with a second set for the last block whose rows past T - 1 are
+// clamped to T - 1 (their scores are masked).  V^T tiles are copied as they are.
+struct AttLoader {
+    const uint8_t *k0;            // K row 0 of this (batch, head)
+    const uint8_t *vt0;           // V^T tile 0 of this (batch, head)
+    int64_t kstep;                // bytes of K per key block
+    uint32_t koff[4], klast[4];   // per-lane K offsets: full blocks, the last block
+    uint32_t voff;                // per-lane V^T offset
+    int lastb;
+};
+
+__device__ __forceinline__ AttLoader att_loader(const AttnArgs &p, int b, int h, int wave, int lane) {
+    AttLoader L;
+    L.k0 = reinterpret_cast<const uint8_t *>(p.k + (int64_t)b * p.T * p.ldk + (int64_t)h * ATT_D);
+    L.vt0 = reinterpret_cast<const uint8_t *>(p.vt + ((int64_t)b * p.H + h) * p.nkb * (ATT_KB * ATT_D));
+    L.kstep = (int64_t)ATT_KB * p.ldk * 2;
+    L.lastb = p.nkb - 1;
+    const int rmax = p.T - 1 - L.lastb * ATT_KB;  // last valid row of the last block
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int n = wave * 4 + j;
-        const int r = 4 * n + (lane >> 4);            // key row in the block
-        int t = kb * ATT_KB + r;
-        t = t < p.T ? t : p.T - 1;                     // rows past the end: masked in the softmax
+        const int r = 4 * (wave * 4 + j) + (lane >> 4);
         const int c = (lane & 15) ^ (r & 15);
-        const uint32_t off = (uint32_t)((((int64_t)b * p.T + t) * p.ldk + (int64_t)h * ATT_D + c * 8) * 2);
-        att_dma16(p.k, off, base + n * 1024);
+        const int rl = r < rmax ? r : rmax;
+        L.koff[j] = (uint32_t)(((int64_t)r * p.ldk + c * 8) * 2);
+        L.klast[j] = (uint32_t)(((int64_t)rl * p.ldk + c * 8) * 2);
     }
-    const uint16_t *tile = p.vt + (((int64_t)b * p.H + h) * p.nkb + kb) * (ATT_KB * ATT_D);
+    L.voff = (uint32_t)(wave * 4096 + lane * 16);
+    return L;
+}
+
+// Issue key block kb (clamped by the caller to the last block) into an LDS slot.
+__device__ __forceinline__ void att_issue(const AttLoader &L, int wave, uint8_t *slot, int kb) {
+    const uint32_t base = att_lds_addr(slot) + wave * 4096;
+    const uint8_t *kp = L.k0 + kb * L.kstep;
+    if (kb == L.lastb) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int n = wave * 4 + j;
-        att_dma16(tile, (uint32_t)(n * 1024 + lane * 16), base + ATT_TILE + n * 1024);
+        for (int j = 0; j < 4; ++j) att_dma16(kp, L.klast[j], base + j * 1024);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) att_dma16(kp, L.koff[j], base + j * 1024);
     }
+    const uint8_t *tile = L.vt0 + (int64_t)kb * ATT_TILE;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) att_dma16(tile, L.voff + j * 1024, base + ATT_TILE + j * 1024);
 }
 
 // K fragments of one 32-key sub-block (half hb of an LDS key block), all 8
@@ -168,21 +195,43 @@ __device__ __forceinline__ void att_mask(f32x16a_t &s, int kbase, int T, int hf)
     }
 }
 
-// Scores above the running reference max m by at most ATT_RESCALE (log2
-// units) are exponentiated against m as they are: P <= 2^ATT_RESCALE, which
-// bf16 P and the fp32 sums hold as well as P <= 1.  Only a sub-block whose max
-// exceeds that moves m (to the sub-block max) and rescales O and l.
-constexpr float ATT_RESCALE = 8.0f;
-
 __device__ __forceinline__ float att_max(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 
-// Online softmax of one 32-query tile over one 32-key sub-block.  In: the raw
-// scores s (this lane's 16 keys of query lq; the other half-wave holds the
-// other 16).  Updates the scaled reference max m and the partial sum l (this
-// lane's keys; the half-waves' sums are added at the end), writes P as the
-// bf16 B operands of the P V product and returns the factor O must be
-// multiplied by before this sub-block's P V.
-__device__ __forceinline__ float att_softmax(const f32x16a_t &s, float &m, float &l, uint4 (&pf)[2], float c) {
+// Keep a softmax inside the region whose MFMAs it runs beside: the compiler
+// would otherwise sink it past the branch that ends the region.
+__device__ __forceinline__ void att_pin(uint4 (&pf)[2], float &x) {
+    u32x4_t v0 = {pf[0].x, pf[0].y, pf[0].z, pf[0].w}, v1 = {pf[1].x, pf[1].y, pf[1].z, pf[1].w};
+    asm volatile("" : "+v"(v0), "+v"(v1), "+v"(x));
+    pf[0] = make_uint4(v0.x, v0.y, v0.z, v0.w);
+    pf[1] = make_uint4(v1.x, v1.y, v1.z, v1.w);
+}
+
+// P = 2^(s c - m) for this lane's 16 keys of query lq, written as the bf16 B
+// operands of the P V product; returns their sum (of the bf16 values used).
+__device__ __forceinline__ float att_exp_pack(const f32x16a_t &s, float m, uint4 (&pf)[2], float c) {
+    const bf16x2_t ones = {(__bf16)1.0f, (__bf16)1.0f};
+    float sum0 = 0.f, sum1 = 0.f;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * u + 2 * e], c, -m));
+            const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * u + 2 * e + 1], c, -m));
+            w[e] = pack_bf16x2(p0, p1);
+        }
+        pf[u] = make_uint4(w[0], w[1], w[2], w[3]);
+        sum0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w[0]), ones, sum0, false);
+        sum1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w[1]), ones, sum1, false);
+        sum0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w[2]), ones, sum0, false);
+        sum1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w[3]), ones, sum1, false);
+    }
+    return sum0 + sum1;
+}
+
+// The (unscaled) row max of a score tile over both half-waves (the other
+// half-wave holds the other 16 keys of the same query).
+__device__ __forceinline__ float att_rowmax(const f32x16a_t &s) {
     float a0 = att_max(s[0], s[1]), a1 = att_max(s[2], s[3]);
 #pragma unroll
     for (int i = 4; i < 16; i += 4) {
@@ -191,36 +240,24 @@ __device__ __forceinline__ float att_softmax(const f32x16a_t &s, float &m, float
     }
     const float mx0 = att_max(a0, a1);
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx0), __float_as_uint(mx0), false, false);
-    const float mx = att_max(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * c;
+    return att_max(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+}
+
+// Online softmax with a running max (the safe form).  Scores above the
+// reference max m by at most ATT_RESCALE (log2 units) are exponentiated
+// against m as they are (P <= 2^ATT_RESCALE); a sub-block whose max exceeds
+// that moves m to its max.  Updates m and the partial sum l (this lane's keys;
+// the half-waves' sums are added at the end) and returns the factor O must be
+// multiplied by before this sub-block's P V.
+constexpr float ATT_RESCALE = 8.0f;
+
+__device__ __forceinline__ float att_softmax(const f32x16a_t &s, float &m, float &l, uint4 (&pf)[2], float c) {
+    const float mx = att_rowmax(s) * c;
     const float mnew = mx > m + ATT_RESCALE ? mx : m;
-    const float alpha = __builtin_amdgcn_exp2f(m - mnew);  // 1 if m stays, 0 on the first sub-block
+    float alpha = __builtin_amdgcn_exp2f(m - mnew);  // 1 if m stays, 0 on the first sub-block
     m = mnew;
-    const bf16x2_t ones = {(__bf16)1.0f, (__bf16)1.0f};
-    float sum0 = 0.f, sum1 = 0.f;
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        uint32_t w[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * u + 2 * e], c, -mnew));
-            const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * u + 2 * e + 1], c, -mnew));
-            w[e] = pack_bf16x2(p0, p1);
-        }
-        pf[u] = make_uint4(w[0], w[1], w[2], w[3]);
-        // l sums the bf16 P that the P V product uses.
-        sum0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w[0]), ones, sum0, false);
-        sum1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w[1]), ones, sum1, false);
-        sum0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w[2]), ones, sum0, false);
-        sum1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w[3]), ones, sum1, false);
-    }
-    l = l * alpha + (sum0 + sum1);
-    // Pin the whole softmax before the rescale branch that follows it, inside
-    // the region whose MFMAs it runs beside (else the compiler sinks the
-    // exponentials past the branch, after those MFMAs).
-    u32x4_t v0 = {pf[0].x, pf[0].y, pf[0].z, pf[0].w}, v1 = {pf[1].x, pf[1].y, pf[1].z, pf[1].w};
-    asm volatile("" : "+v"(v0), "+v"(v1), "+v"(l));
-    pf[0] = make_uint4(v0.x, v0.y, v0.z, v0.w);
-    pf[1] = make_uint4(v1.x, v1.y, v1.z, v1.w);
+    l = l * alpha + att_exp_pack(s, mnew, pf, c);
+    att_pin(pf, alpha);
     return alpha;
 }
 
@@ -230,6 +267,26 @@ __device__ __forceinline__ void att_rescale(f32x16a_t (&o)[4], float alpha) {
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
     }
+}
+
+// The softmax of one region.  FIXED: against the reference max m fixed by
+// the tile's first sub-block (no max, no rescale: l += sum, nothing to branch
+// on); otherwise the safe form above.  att_sm_end runs after the region's
+// instruction interleave.
+template <bool FIXED>
+__device__ __forceinline__ float att_sm(const f32x16a_t &s, float &m, float &l, uint4 (&pf)[2], float c) {
+    if constexpr (FIXED) {
+        float sum = att_exp_pack(s, m, pf, c);
+        att_pin(pf, sum);
+        return sum;
+    } else {
+        return att_softmax(s, m, l, pf, c);
+    }
+}
+template <bool FIXED>
+__device__ __forceinline__ void att_sm_end(f32x16a_t (&o)[4], float &l, float r) {
+    if constexpr (FIXED) l += r;
+    else att_rescale(o, r);
 }
 
 // Instruction interleave of one region: N MFMAs, each followed by up to V
@@ -244,19 +301,145 @@ __device__ __forceinline__ void att_interleave() {
     }
 }
 
-// Per wave: 64 queries in two 32-query tiles (0, 1), keys in 32-key
-// sub-blocks u (two per 64-key LDS block).  Per sub-block the work is S_t =
-// K Q_t^T, the softmax SM_t and O_t += V^T P_t^T; it runs software-pipelined
-// in two steps so that each softmax runs on the vector ALU beside 16 MFMAs
-// that do not depend on it:
+// One pass over all keys for this wave's 64 queries: two 32-query tiles
+// (0, 1), keys in 32-key sub-blocks u (two per 64-key LDS block).  Per
+// sub-block the work is S_t = K Q_t^T, the softmax SM_t and O_t += V^T P_t^T;
+// it runs software-pipelined in two steps so that each softmax runs on the
+// vector ALU beside 16 MFMAs that do not depend on it:
 //   X(u): MFMA S_1(u), PV_1(u-1)   | VALU SM_0(u) | LDS reads of V^T(u), K(u+1)
 //   Y(u): MFMA PV_0(u), S_0(u+1)   | VALU SM_1(u)
 // Every K and V^T fragment is read from LDS once and used for both query
 // tiles; the fragments alternate between two register sets by the parity of u.
 // LDS holds four 64-key blocks: block n + 2 is issued into the slot of block
 // n - 2 at the barrier before X(2n - 1), after the last read of that slot.
+//
+// FAST: after each tile's first sub-block (which sets m to its max) the
+// reference max stays fixed, so a region has no max, no rescale and no branch.
+// P may then exceed 1 by the growth of the scores past the first sub-block's
+// max; the caller checks that l stayed below ATT_FAST_LMAX (so that P, l and O
+// stayed finite) and otherwise reruns the pass with FAST = false.
+template <bool FAST>
+__device__ __forceinline__ void att_pass(const AttnArgs &p, const AttLoader &ld, uint8_t *lds, const uint4 (&qf)[2][8],
+                                         int wave, int lq, int hf, f32x16a_t (&o0)[4], f32x16a_t (&o1)[4], float &l0,
+                                         float &l1) {
+    const int nkb = p.nkb, lastb = nkb - 1;
+    // Keys past T exist only in the last block; a sub-block there may be all
+    // masked, which gives P = 0 and leaves m, l and O as they are.
+    const bool ragged = (p.T & (ATT_KB - 1)) != 0;
+    const float c = p.scale_log2e;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) att_issue(ld, wave, lds + i * ATT_STAGE, i < nkb ? i : lastb);
+
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) o0[dt] = o1[dt] = f32x16a_t{};
+    float m0 = -__builtin_inff(), m1 = -__builtin_inff();
+    l0 = l1 = 0.f;
+    uint4 kfa[8], kfb[8], vfa[2][4], vfb[2][4], pf0[2], pf1[2];
+    f32x16a_t s0, s1;
+    auto slot = [&](int n) { return lds + (n & 3) * ATT_STAGE; };
+
+    // Block 0 landed for every wave.  S_0(0); X(0) without a P V, whose
+    // softmax (the safe form) sets tile 0's reference max; in a FAST pass
+    // tile 1's is set here from S_1(0) as well.
+    att_wait_vmcnt<16>();
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    att_read_k(kfa, lds, 0, lq, hf);
+    att_scores(s0, kfa, qf[0]);
+    if (lastb == 0 && ragged) att_mask(s0, 0, p.T, hf);
+    {
+        att_scores(s1, kfa, qf[1]);
+        const float r = att_sm<false>(s0, m0, l0, pf0, c);
+        att_read_v(vfa, slot(0) + ATT_TILE, 0, lq, hf);
+        att_read_k(kfb, slot(0), 1, lq, hf);
+        att_interleave<8, 8, 2>();
+        att_sm_end<false>(o0, l0, r);
+    }
+    if (FAST) {
+        if (lastb == 0 && ragged) att_mask(s1, 0, p.T, hf);
+        m1 = att_rowmax(s1) * c;
+    }
+    // Block n: sub-blocks u = 2n (fragments in the "a" registers) and 2n + 1 ("b").
+    for (int n = 0; n < lastb; ++n) {
+        // ---- Y(2n): P V with vfa, next scores with kfb
+        {
+            att_pv(o0, vfa, pf0);
+            att_scores(s0, kfb, qf[0]);
+            const float r = att_sm<FAST>(s1, m1, l1, pf1, c);
+            att_interleave<16, 4, 0>();
+            att_sm_end<FAST>(o1, l1, r);
+        }
+        // Block n + 1 (K of sub-block 2n + 2, read in X(2n + 1)) landed for
+        // every wave; the slot of block n - 1 is free: issue block n + 3 there.
+        att_wait_vmcnt<8>();
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        att_issue(ld, wave, slot(n + 3), n + 3 < nkb ? n + 3 : lastb);
+        // ---- X(2n + 1): scores with kfb, P V with vfa; reads vfb, kfa
+        {
+            att_scores(s1, kfb, qf[1]);
+            att_pv(o1, vfa, pf1);
+            const float r = att_sm<FAST>(s0, m0, l0, pf0, c);
+            att_read_v(vfb, slot(n) + ATT_TILE, 1, lq, hf);
+            att_read_k(kfa, slot(n + 1), 0, lq, hf);
+            att_interleave<16, 4, 1>();
+            att_sm_end<FAST>(o0, l0, r);
+        }
+        // ---- Y(2n + 1): P V with vfb, next scores with kfa
+        {
+            att_pv(o0, vfb, pf0);
+            att_scores(s0, kfa, qf[0]);
+            const float r = att_sm<FAST>(s1, m1, l1, pf1, c);
+            att_interleave<16, 4, 0>();
+            att_sm_end<FAST>(o1, l1, r);
+        }
+        if (n + 1 == lastb && ragged) att_mask(s0, (n + 1) * ATT_KB, p.T, hf);
+        // ---- X(2n + 2): scores with kfa, P V with vfb; reads vfa, kfb
+        {
+            att_scores(s1, kfa, qf[1]);
+            att_pv(o1, vfb, pf1);
+            const float r = att_sm<FAST>(s0, m0, l0, pf0, c);
+            att_read_v(vfa, slot(n + 1) + ATT_TILE, 0, lq, hf);
+            att_read_k(kfb, slot(n + 1), 1, lq, hf);
+            att_interleave<16, 4, 1>();
+            att_sm_end<FAST>(o0, l0, r);
+        }
+    }
+    // Last block L: Y(2L), X(2L + 1), Y(2L + 1) and PV_1(2L + 1); its data
+    // landed at the last barrier (or the first), no further loads.
+    if (ragged) att_mask(s1, lastb * ATT_KB, p.T, hf);
+    {
+        att_pv(o0, vfa, pf0);
+        att_scores(s0, kfb, qf[0]);
+        const float r = att_sm<FAST>(s1, m1, l1, pf1, c);
+        att_interleave<16, 4, 0>();
+        att_sm_end<FAST>(o1, l1, r);
+    }
+    if (ragged) att_mask(s0, lastb * ATT_KB + 32, p.T, hf);
+    {
+        att_scores(s1, kfb, qf[1]);
+        att_pv(o1, vfa, pf1);
+        const float r = att_sm<FAST>(s0, m0, l0, pf0, c);
+        att_read_v(vfb, slot(lastb) + ATT_TILE, 1, lq, hf);
+        att_interleave<16, 4, 1>();
+        att_sm_end<FAST>(o0, l0, r);
+    }
+    if (ragged) att_mask(s1, lastb * ATT_KB + 32, p.T, hf);
+    {
+        att_pv(o0, vfb, pf0);
+        const float r = att_sm<FAST>(s1, m1, l1, pf1, c);
+        att_interleave<8, 8, 0>();
+        att_sm_end<FAST>(o1, l1, r);
+    }
+    att_pv(o1, vfb, pf1);
+    att_wait_vmcnt<0>();  // the clamped tail loads land before the LDS is reused or released
+}
+
+// Bound on a lane's partial sum l after a FAST pass: below it, every P and
+// every |O| (for |V| < 2^63) stayed finite.
+constexpr float ATT_FAST_LMAX = 18446744073709551616.0f;  // 2^64
+
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_attn_fwd(AttnArgs p) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
+    __shared__ int redo[4];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lq = lane & 31, hf = lane >> 5;
@@ -288,7 +471,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         for (int j = 0; j < 8; ++j) qf[t][j] = *reinterpret_cast<const uint4 *>(qrow + 16 * j);
     }
     // Q^T is only ever an MFMA operand: keep it in accumulation registers, which
-    // leaves the architectural ones to the K / V^T fragments, P and the softmax.
+    // leaves the architectural ones to O, the scores, P and the softmax.
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -298,110 +481,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             qf[t][j] = make_uint4(v.x, v.y, v.z, v.w);
         }
 
-    const int nkb = p.nkb, lastb = nkb - 1;
-    // Keys past T exist only in the last block; a sub-block there may be all
-    // masked, which gives P = 0 and leaves m, l and O as they are.
-    const bool ragged = (p.T & (ATT_KB - 1)) != 0;
-    const float c = p.scale_log2e;
-#pragma unroll
-    for (int i = 0; i < 3; ++i) att_issue(p, b, h, wave, lane, lds + i * ATT_STAGE, i < nkb ? i : lastb);
-
+    const AttLoader ld = att_loader(p, b, h, wave, lane);
     f32x16a_t o0[4], o1[4];
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) o0[dt] = o1[dt] = f32x16a_t{};
-    float m0 = -__builtin_inff(), m1 = -__builtin_inff(), l0 = 0.f, l1 = 0.f;
-    uint4 kfa[8], kfb[8], vfa[2][4], vfb[2][4], pf0[2], pf1[2];
-    f32x16a_t s0, s1;
-    auto slot = [&](int n) { return lds + (n & 3) * ATT_STAGE; };
-
-    // Prologue: block 0 landed for every wave; S_0(0); X(0) without a P V.
-    att_wait_vmcnt<16>();
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    att_read_k(kfa, lds, 0, lq, hf);
-    att_scores(s0, kfa, qf[0]);
-    if (lastb == 0 && ragged) att_mask(s0, 0, p.T, hf);
-    {
-        att_scores(s1, kfa, qf[1]);
-        const float alpha = att_softmax(s0, m0, l0, pf0, c);
-        att_read_v(vfa, slot(0) + ATT_TILE, 0, lq, hf);
-        att_read_k(kfb, slot(0), 1, lq, hf);
-        att_interleave<8, 8, 2>();
-        att_rescale(o0, alpha);
-    }
-    // Block n: sub-blocks u = 2n (fragments in the "a" registers) and 2n + 1 ("b").
-    for (int n = 0; n < lastb; ++n) {
-        const bool mask_next = n + 1 == lastb && ragged;
-        // ---- Y(2n): P V with vfa, next scores with kfb
-        {
-            att_pv(o0, vfa, pf0);
-            att_scores(s0, kfb, qf[0]);
-            const float alpha = att_softmax(s1, m1, l1, pf1, c);
-            att_interleave<16, 4, 0>();
-            att_rescale(o1, alpha);
-        }
-        // Block n + 1 (K of sub-block 2n + 2, read in X(2n + 1)) landed for
-        // every wave; the slot of block n - 1 is free: issue block n + 3 there.
-        att_wait_vmcnt<8>();
-        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        att_issue(p, b, h, wave, lane, slot(n + 3), n + 3 < nkb ? n + 3 : lastb);
-        // ---- X(2n + 1): scores with kfb, P V with vfa; reads vfb, kfa
-        {
-            att_scores(s1, kfb, qf[1]);
-            att_pv(o1, vfa, pf1);
-            const float alpha = att_softmax(s0, m0, l0, pf0, c);
-            att_read_v(vfb, slot(n) + ATT_TILE, 1, lq, hf);
-            att_read_k(kfa, slot(n + 1), 0, lq, hf);
-            att_interleave<16, 4, 1>();
-            att_rescale(o0, alpha);
-        }
-        // ---- Y(2n + 1): P V with vfb, next scores with kfa
-        {
-            att_pv(o0, vfb, pf0);
-            att_scores(s0, kfa, qf[0]);
-            const float alpha = att_softmax(s1, m1, l1, pf1, c);
-            att_interleave<16, 4, 0>();
-            att_rescale(o1, alpha);
-        }
-        if (mask_next) att_mask(s0, (n + 1) * ATT_KB, p.T, hf);
-        // ---- X(2n + 2): scores with kfa, P V with vfb; reads vfa, kfb
-        {
-            att_scores(s1, kfa, qf[1]);
-            att_pv(o1, vfb, pf1);
-            const float alpha = att_softmax(s0, m0, l0, pf0, c);
-            att_read_v(vfa, slot(n + 1) + ATT_TILE, 0, lq, hf);
-            att_read_k(kfb, slot(n + 1), 1, lq, hf);
-            att_interleave<16, 4, 1>();
-            att_rescale(o0, alpha);
-        }
-    }
-    // Last block: Y(2L), X(2L + 1), Y(2L + 1) and PV_1(2L + 1); its data landed
-    // at the last barrier (or the prologue's), no further loads.
-    if (ragged) att_mask(s1, lastb * ATT_KB, p.T, hf);
-    {
-        att_pv(o0, vfa, pf0);
-        att_scores(s0, kfb, qf[0]);
-        const float alpha = att_softmax(s1, m1, l1, pf1, c);
-        att_interleave<16, 4, 0>();
-        att_rescale(o1, alpha);
-    }
-    if (ragged) att_mask(s0, lastb * ATT_KB + 32, p.T, hf);
-    {
-        att_scores(s1, kfb, qf[1]);
-        att_pv(o1, vfa, pf1);
-        const float alpha = att_softmax(s0, m0, l0, pf0, c);
-        att_read_v(vfb, slot(lastb) + ATT_TILE, 1, lq, hf);
-        att_interleave<16, 4, 1>();
-        att_rescale(o0, alpha);
-    }
-    if (ragged) att_mask(s1, lastb * ATT_KB + 32, p.T, hf);
-    {
-        att_pv(o0, vfb, pf0);
-        const float alpha = att_softmax(s1, m1, l1, pf1, c);
-        att_interleave<8, 8, 0>();
-        att_rescale(o1, alpha);
-    }
-    att_pv(o1, vfb, pf1);
-    att_wait_vmcnt<0>();  // the clamped tail loads land before the workgroup ends
+    float l0, l1;
+    att_pass<true>(p, ld, lds, qf, wave, lq, hf, o0, o1, l0, l1);
+    // Rerun the whole workgroup in the safe form when any wave's sums left
+    // the range the fixed reference max guarantees (scores that grew by more
+    // than ~64 in log2 units past their first sub-block's max).
+    if (threadIdx.x % 64 == 0) redo[wave] = 0;
+    const bool bad = !(l0 < ATT_FAST_LMAX && l1 < ATT_FAST_LMAX);
+    if (__builtin_amdgcn_ballot_w64(bad) && lane == 0) redo[wave] = 1;
+    __syncthreads();
+    if (redo[0] | redo[1] | redo[2] | redo[3]) att_pass<false>(p, ld, lds, qf, wave, lq, hf, o0, o1, l0, l1);
 
     // O = O^T / l: lane (q, hf) holds dims 32dt + 8(i/4) + 4hf + i%4 of its query.
 #pragma unroll

@@ -62,6 +62,33 @@ def test_attention_on_fused_qkv_views(dev):
     check(out, reference(q, k, v, 0.1))
 
 
+@pytest.mark.parametrize("jump", [30.0, 400.0])
+def test_attention_score_jump_past_first_block(dev, jump):
+    """Keys whose scores exceed the scores of the first 32 keys by about
+    `jump` (natural-log units).  The kernel's first pass keeps each query's
+    reference max from its first key sub-block: a jump of 30 stays within
+    its range (P up to ~e^33, l and O finite), one of 400 overflows it, which
+    the kernel detects and redoes in the running-max form.  Either way the
+    output equals the reference."""
+    b, s, t, h = 1, 256, 700, 2
+    say("attention score jump", jump)
+    g = torch.Generator().manual_seed(int(jump))
+    # Head 0: every query is q0 plus a little noise; keys 600..609 are q0
+    # scaled to a logit of about `jump` against it.
+    q0 = bf16_randn(g, (128,)).float()
+    q = (q0 + 0.05 * bf16_randn(g, (b, s, h, 128)).float()).to(torch.bfloat16)
+    k = bf16_randn(g, (b, t, h, 128))
+    v = bf16_randn(g, (b, t, h, 128))
+    scale = 128 ** -0.5
+    k[0, 600:610, 0] = (q0 * (jump / (scale * q0.square().sum().item()))).to(torch.bfloat16)
+    q, k, v = q.to(dev), k.to(dev), v.to(dev)
+    out = attention.attention(q, k, v)
+    torch.cuda.synchronize()
+    ref = reference(q, k, v, scale)
+    assert torch.isfinite(out.float()).all()
+    check(out, ref)
+
+
 def test_attention_rejects_other_head_dims(dev):
     from qwen_image_accel import _native
     x = torch.zeros(1, 8, 1, 64, dtype=torch.bfloat16, device=dev)
