@@ -7,7 +7,8 @@ BASELINE.json: the fused QK-RMSNorm + 3-axis RoPE at the 1024^2 shape
 (Q, K bf16 [1, 4352, 24, 128]), reported as algorithmic HBM GB/s.  The other
 configurations (AdaLN @512^2, SwiGLU, gated residual, MXFP8 quantize, MXFP8
 GEMM + bias, the block minus attention @2048^2 and µs/block @1024^2) are
-measured in the same run and reported under "components".
+measured in the same run and reported under "components", with the attention
+core at both shapes and the whole block @1024^2 attention included.
 
 Timing: each step is one pass of the op over one batch of synthetic input
 already resident in device memory.  The K timed steps are captured in a HIP
@@ -34,6 +35,7 @@ import torch  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 MXFP8_PEAK_TFLOPS = 5000.0     # MI355X dense MXFP8 MFMA (5.0 PFLOP/s)
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA (2.5 PFLOP/s)
 MALL_BYTES = 256 << 20         # Infinity Cache
 METRIC = json.load(open(os.path.join(ROOT, "BASELINE.json")))["metric"]
 
@@ -260,8 +262,35 @@ def bench_gemm(steps, warmup, tiled=True):
                 shape="4352x3072x12288 +bias", layout="tiled" if tiled else "row-major")
 
 
-def bench_block(tokens, steps, warmup):
-    """Config 5 / µs-per-block: one MMDiT block minus the attention core."""
+def bench_attention(tokens, steps, warmup):
+    """The block's attention core: softmax(Q K^T / sqrt(128)) V over one
+    image's joint sequence (S = T = tokens, 24 heads x 128), Q, K, V as column
+    blocks of the fused QKV projection [1, S, 3*3072] bf16 ~N(0,1); bf16 MFMA
+    with fp32 softmax and accumulation.  Flops: 4 S T 128 per head (Q K^T and
+    P V), as attention benchmarks count them."""
+    from qwen_image_accel import _native
+    H, D = 24, 128
+    g = gen(7)
+    qkv = randn(g, (1, tokens, 3 * H * D))
+    out = torch.empty(1, tokens, H * D, dtype=torch.bfloat16, device="cuda")
+    L = _native.lib()
+    ws = torch.empty(L.qim_attention_workspace_bytes(1, tokens, H, D) // 2, dtype=torch.bfloat16, device="cuda")
+    base, row = qkv.data_ptr(), 3 * H * D
+
+    def step(i):
+        rc = L.qim_attention(base, row, base + H * D * 2, row, base + 2 * H * D * 2, row, out.data_ptr(), H * D,
+                             ws.data_ptr(), 1, tokens, tokens, H, D, D ** -0.5, torch.cuda.current_stream().cuda_stream)
+        assert rc == 0
+    us = Timed(step, max(3, steps // 20), warmup).run() * 1e3
+    flops = 4.0 * tokens * tokens * D * H
+    tf = flops / us / 1e6
+    return dict(kernel="k_attn_fwd", us=us, flops=flops, tflops=tf, frac=tf / BF16_PEAK_TFLOPS,
+                shape=f"S=T={tokens}, 24x128")
+
+
+def bench_block(tokens, steps, warmup, with_attention=False):
+    """Config 5 / µs-per-block: one MMDiT block minus the attention core
+    (with_attention: the whole block, the attention core included)."""
     from qwen_image_accel import rope
     from qwen_image_accel.block import MMDiTBlock
     g = gen(42)
@@ -271,8 +300,13 @@ def bench_block(tokens, steps, warmup):
     mod = randn(g, (1, 6, 3072), 0.1)
     freqs = rope.image_table(256, side, side, "cuda")
 
+    attn = None
+    if with_attention:
+        from qwen_image_accel.kernels import attention
+        attn = attention.attention
+
     def step(i):
-        blk.forward(h, mod, freqs)
+        blk.forward(h, mod, freqs, attention_fn=attn)
     us = Timed(step, max(3, steps // 20), warmup).run() * 1e3
     flops = blk.flops(tokens)
     return dict(us=us, flops=flops, tflops=flops / us / 1e6, tokens=tokens,
@@ -349,7 +383,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(every hot-path op is token-row independent; see the sharding note in DESIGN.md).",
+              "(every hot-path op is token-row independent, so token rows would shard across GPUs with no exchange).",
               file=sys.stderr)
         sys.exit(2)
     assert torch.cuda.is_available(), "bench.py needs a GPU"
@@ -371,6 +405,9 @@ def main():
                      ("mxfp8_gemm_bias_1024_rowmajor", lambda: bench_gemm(steps, warm, tiled=False)),
                      ("block_1024", lambda: bench_block(4352, steps, warm)),
                      ("block_2048", lambda: bench_block(16640, steps, warm)),
+                     ("attention_1024", lambda: bench_attention(4352, steps, warm)),
+                     ("attention_2048", lambda: bench_attention(16640, steps, warm)),
+                     ("block_1024_with_attention", lambda: bench_block(4352, steps, warm, with_attention=True)),
                      ("copy_256MiB", lambda: bench_copy(steps, warm)),
                      # copies moving the algorithmic bytes of each bandwidth-bound config
                      ("copy_23.6MB", lambda: bench_copy(steps, warm, 23611392 // 2, "23.6 MB moved")),
