@@ -271,8 +271,8 @@ __device__ __forceinline__ void att_rescale(f32x16a_t (&o)[4], float alpha) {
 
 // The softmax of one region.  FIXED: against the reference max m fixed by
 // the tile's first sub-block (no max, no rescale: l += sum, nothing to branch
-// on); otherwise the safe form above.  att_sm_end runs after the region's
-// instruction interleave.
+// on); otherwise the safe form above.  att_sm_end runs at the region's end,
+// after its LDS reads are issued.
 template <bool FIXED>
 __device__ __forceinline__ float att_sm(const f32x16a_t &s, float &m, float &l, uint4 (&pf)[2], float c) {
     if constexpr (FIXED) {
@@ -287,18 +287,6 @@ template <bool FIXED>
 __device__ __forceinline__ void att_sm_end(f32x16a_t (&o)[4], float &l, float r) {
     if constexpr (FIXED) l += r;
     else att_rescale(o, r);
-}
-
-// Instruction interleave of one region: N MFMAs, each followed by up to V
-// vector-ALU (incl. transcendental) and R LDS-read instructions.
-template <int N, int V, int R>
-__device__ __forceinline__ void att_interleave() {
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        if (R > 0) __builtin_amdgcn_sched_group_barrier(0x100, R, 0);
-        __builtin_amdgcn_sched_group_barrier(0x402, V, 0);
-    }
 }
 
 // One pass over all keys for this wave's 64 queries: two 32-query tiles
@@ -351,7 +339,6 @@ __device__ __forceinline__ void att_pass(const AttnArgs &p, const AttLoader &ld,
         const float r = att_sm<false>(s0, m0, l0, pf0, c);
         att_read_v(vfa, slot(0) + ATT_TILE, 0, lq, hf);
         att_read_k(kfb, slot(0), 1, lq, hf);
-        att_interleave<8, 8, 2>();
         att_sm_end<false>(o0, l0, r);
     }
     if (FAST) {
@@ -365,7 +352,6 @@ __device__ __forceinline__ void att_pass(const AttnArgs &p, const AttLoader &ld,
             att_pv(o0, vfa, pf0);
             att_scores(s0, kfb, qf[0]);
             const float r = att_sm<FAST>(s1, m1, l1, pf1, c);
-            att_interleave<16, 4, 0>();
             att_sm_end<FAST>(o1, l1, r);
         }
         // Block n + 1 (K of sub-block 2n + 2, read in X(2n + 1)) landed for
@@ -380,7 +366,6 @@ __device__ __forceinline__ void att_pass(const AttnArgs &p, const AttLoader &ld,
             const float r = att_sm<FAST>(s0, m0, l0, pf0, c);
             att_read_v(vfb, slot(n) + ATT_TILE, 1, lq, hf);
             att_read_k(kfa, slot(n + 1), 0, lq, hf);
-            att_interleave<16, 4, 1>();
             att_sm_end<FAST>(o0, l0, r);
         }
         // ---- Y(2n + 1): P V with vfb, next scores with kfa
@@ -388,7 +373,6 @@ __device__ __forceinline__ void att_pass(const AttnArgs &p, const AttLoader &ld,
             att_pv(o0, vfb, pf0);
             att_scores(s0, kfa, qf[0]);
             const float r = att_sm<FAST>(s1, m1, l1, pf1, c);
-            att_interleave<16, 4, 0>();
             att_sm_end<FAST>(o1, l1, r);
         }
         if (n + 1 == lastb && ragged) att_mask(s0, (n + 1) * ATT_KB, p.T, hf);
@@ -399,7 +383,6 @@ __device__ __forceinline__ void att_pass(const AttnArgs &p, const AttLoader &ld,
             const float r = att_sm<FAST>(s0, m0, l0, pf0, c);
             att_read_v(vfa, slot(n + 1) + ATT_TILE, 0, lq, hf);
             att_read_k(kfb, slot(n + 1), 1, lq, hf);
-            att_interleave<16, 4, 1>();
             att_sm_end<FAST>(o0, l0, r);
         }
     }
@@ -410,7 +393,6 @@ __device__ __forceinline__ void att_pass(const AttnArgs &p, const AttLoader &ld,
         att_pv(o0, vfa, pf0);
         att_scores(s0, kfb, qf[0]);
         const float r = att_sm<FAST>(s1, m1, l1, pf1, c);
-        att_interleave<16, 4, 0>();
         att_sm_end<FAST>(o1, l1, r);
     }
     if (ragged) att_mask(s0, lastb * ATT_KB + 32, p.T, hf);
@@ -419,14 +401,12 @@ __device__ __forceinline__ void att_pass(const AttnArgs &p, const AttLoader &ld,
         att_pv(o1, vfa, pf1);
         const float r = att_sm<FAST>(s0, m0, l0, pf0, c);
         att_read_v(vfb, slot(lastb) + ATT_TILE, 1, lq, hf);
-        att_interleave<16, 4, 1>();
         att_sm_end<FAST>(o0, l0, r);
     }
     if (ragged) att_mask(s1, lastb * ATT_KB + 32, p.T, hf);
     {
         att_pv(o0, vfb, pf0);
         const float r = att_sm<FAST>(s1, m1, l1, pf1, c);
-        att_interleave<8, 8, 0>();
         att_sm_end<FAST>(o1, l1, r);
     }
     att_pv(o1, vfb, pf1);
