@@ -274,12 +274,14 @@ def bench_attention(tokens, steps, warmup):
     qkv = randn(g, (1, tokens, 3 * H * D))
     out = torch.empty(1, tokens, H * D, dtype=torch.bfloat16, device="cuda")
     L = _native.lib()
-    ws = torch.empty(L.qim_attention_workspace_bytes(1, tokens, H, D) // 2, dtype=torch.bfloat16, device="cuda")
+    nbytes = L.qim_attention_workspace_bytes(1, tokens, tokens, H, D)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
     base, row = qkv.data_ptr(), 3 * H * D
 
     def step(i):
         rc = L.qim_attention(base, row, base + H * D * 2, row, base + 2 * H * D * 2, row, out.data_ptr(), H * D,
-                             ws.data_ptr(), 1, tokens, tokens, H, D, D ** -0.5, torch.cuda.current_stream().cuda_stream)
+                             ws.data_ptr(), nbytes, 1, tokens, tokens, H, D, D ** -0.5,
+                             torch.cuda.current_stream().cuda_stream)
         assert rc == 0
     us = Timed(step, max(3, steps // 20), warmup).run() * 1e3
     flops = 4.0 * tokens * tokens * D * H

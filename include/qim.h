@@ -189,16 +189,18 @@ int qim_mxfp8_gemm_qk_norm_rope(const void *aq, const void *as, const void *bq, 
 
 /* Attention core, the block's softmax(Q K^T * scale) V per (batch, head) over
  * [prefix + target] keys (SDPA in the reference: optimizations/
- * quantized_decode.py:70-77).  q: (B, S, H, D), k, v:
- * (B, T, H, D), o: (B, S, H, D), bf16, with ldq / ldk / ldv / ldo elements
- * between consecutive tokens (views into a fused QKV output are fine).  D = 128.
- * scale > 0.  fp32 scores, softmax and accumulation; P rounded to bf16 for
- * the P V product.  vt_workspace: qim_attention_workspace_bytes(B, T, H, D) bytes,
- * 16-byte aligned (V transposed in 64-key tiles). */
+ * quantized_decode.py:70-77).  q: (B, S, H, D), k, v: (B, T, H, D), o:
+ * (B, S, H, D), bf16, with ldq / ldk / ldv / ldo elements between consecutive
+ * tokens (views into a fused QKV output are fine).  D = 128, scale > 0.  fp32
+ * scores, softmax and accumulation; P rounded to bf16 for the P V product.
+ * workspace: at least qim_attention_workspace_bytes(B, S, T, H, D) bytes,
+ * 16-byte aligned, passed with its size (V transposed in 64-key tiles, and
+ * the partial results of work items split over key ranges to fill the last
+ * round of workgroups; the split depends on the current device's CU count). */
 int qim_attention(const void *q, int64_t ldq, const void *k, int64_t ldk, const void *v, int64_t ldv,
-                  void *o, int64_t ldo, void *vt_workspace, int64_t B, int64_t S, int64_t T, int64_t H,
-                  int64_t D, float scale, void *stream);
-int64_t qim_attention_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D);
+                  void *o, int64_t ldo, void *workspace, int64_t workspace_bytes, int64_t B, int64_t S,
+                  int64_t T, int64_t H, int64_t D, float scale, void *stream);
+int64_t qim_attention_workspace_bytes(int64_t B, int64_t S, int64_t T, int64_t H, int64_t D);
 
 /* Test hooks: the device conversions every kernel uses, applied elementwise
  * (fp32 -> E4M3 code; fp32 -> bf16 bits), and one scaled MFMA

@@ -45,6 +45,14 @@ struct AttnArgs {
     uint16_t *o;
     int64_t ldq, ldk, ldo;  // elements between consecutive tokens
     int S, T, H, nkb;       // queries, keys, heads, key blocks
+    int nq;                 // query blocks per (batch, head)
+    // Work split (att_plan): workgroups [0, nfull) each run one whole work item
+    // (query block, head, batch); the remaining ntail items run as nsplit
+    // chunks of kbc key blocks each, writing partial results (part_o: fp32
+    // unnormalised O^T rows, part_ml: (m, l) per query) that k_attn_merge
+    // combines.
+    int nfull, ntail, nsplit, kbc;
+    float *part_o, *part_ml;
     float scale_log2e;
 };
 
@@ -308,19 +316,21 @@ __device__ __forceinline__ void att_sm_end(f32x16a_t (&o)[4], float &l, float r)
 // stayed finite) and otherwise reruns the pass with FAST = false.
 template <bool FAST>
 __device__ __forceinline__ void att_pass(const AttnArgs &p, const AttLoader &ld, uint8_t *lds, const uint4 (&qf)[2][8],
-                                         int wave, int lq, int hf, f32x16a_t (&o0)[4], f32x16a_t (&o1)[4], float &l0,
-                                         float &l1) {
-    const int nkb = p.nkb, lastb = nkb - 1;
-    // Keys past T exist only in the last block; a sub-block there may be all
-    // masked, which gives P = 0 and leaves m, l and O as they are.
-    const bool ragged = (p.T & (ATT_KB - 1)) != 0;
+                                         int wave, int lq, int hf, int kb0, int nkb, f32x16a_t (&o0)[4],
+                                         f32x16a_t (&o1)[4], float &m0, float &m1, float &l0, float &l1) {
+    // Key blocks [kb0, kb0 + nkb); n below counts from kb0.  Keys past T exist
+    // only in the last block of T; a sub-block there may be all masked, which
+    // gives P = 0 and leaves m, l and O as they are.
+    const int lastb = nkb - 1;
+    const bool ragged = kb0 + nkb == p.nkb && (p.T & (ATT_KB - 1)) != 0;
+    const int key0 = kb0 * ATT_KB;
     const float c = p.scale_log2e;
 #pragma unroll
-    for (int i = 0; i < 3; ++i) att_issue(ld, wave, lds + i * ATT_STAGE, i < nkb ? i : lastb);
+    for (int i = 0; i < 3; ++i) att_issue(ld, wave, lds + i * ATT_STAGE, kb0 + (i < nkb ? i : lastb));
 
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) o0[dt] = o1[dt] = f32x16a_t{};
-    float m0 = -__builtin_inff(), m1 = -__builtin_inff();
+    m0 = m1 = -__builtin_inff();
     l0 = l1 = 0.f;
     uint4 kfa[8], kfb[8], vfa[2][4], vfb[2][4], pf0[2], pf1[2];
     f32x16a_t s0, s1;
@@ -333,7 +343,7 @@ __device__ __forceinline__ void att_pass(const AttnArgs &p, const AttLoader &ld,
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     att_read_k(kfa, lds, 0, lq, hf);
     att_scores(s0, kfa, qf[0]);
-    if (lastb == 0 && ragged) att_mask(s0, 0, p.T, hf);
+    if (lastb == 0 && ragged) att_mask(s0, key0, p.T, hf);
     {
         att_scores(s1, kfa, qf[1]);
         const float r = att_sm<false>(s0, m0, l0, pf0, c);
@@ -342,7 +352,7 @@ __device__ __forceinline__ void att_pass(const AttnArgs &p, const AttLoader &ld,
         att_sm_end<false>(o0, l0, r);
     }
     if (FAST) {
-        if (lastb == 0 && ragged) att_mask(s1, 0, p.T, hf);
+        if (lastb == 0 && ragged) att_mask(s1, key0, p.T, hf);
         m1 = att_rowmax(s1) * c;
     }
     // Block n: sub-blocks u = 2n (fragments in the "a" registers) and 2n + 1 ("b").
@@ -358,7 +368,7 @@ __device__ __forceinline__ void att_pass(const AttnArgs &p, const AttLoader &ld,
         // every wave; the slot of block n - 1 is free: issue block n + 3 there.
         att_wait_vmcnt<8>();
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        att_issue(ld, wave, slot(n + 3), n + 3 < nkb ? n + 3 : lastb);
+        att_issue(ld, wave, slot(n + 3), kb0 + (n + 3 < nkb ? n + 3 : lastb));
         // ---- X(2n + 1): scores with kfb, P V with vfa; reads vfb, kfa
         {
             att_scores(s1, kfb, qf[1]);
@@ -375,7 +385,7 @@ __device__ __forceinline__ void att_pass(const AttnArgs &p, const AttLoader &ld,
             const float r = att_sm<FAST>(s1, m1, l1, pf1, c);
             att_sm_end<FAST>(o1, l1, r);
         }
-        if (n + 1 == lastb && ragged) att_mask(s0, (n + 1) * ATT_KB, p.T, hf);
+        if (n + 1 == lastb && ragged) att_mask(s0, key0 + (n + 1) * ATT_KB, p.T, hf);
         // ---- X(2n + 2): scores with kfa, P V with vfb; reads vfa, kfb
         {
             att_scores(s1, kfa, qf[1]);
@@ -388,14 +398,14 @@ __device__ __forceinline__ void att_pass(const AttnArgs &p, const AttLoader &ld,
     }
     // Last block L: Y(2L), X(2L + 1), Y(2L + 1) and PV_1(2L + 1); its data
     // landed at the last barrier (or the first), no further loads.
-    if (ragged) att_mask(s1, lastb * ATT_KB, p.T, hf);
+    if (ragged) att_mask(s1, key0 + lastb * ATT_KB, p.T, hf);
     {
         att_pv(o0, vfa, pf0);
         att_scores(s0, kfb, qf[0]);
         const float r = att_sm<FAST>(s1, m1, l1, pf1, c);
         att_sm_end<FAST>(o1, l1, r);
     }
-    if (ragged) att_mask(s0, lastb * ATT_KB + 32, p.T, hf);
+    if (ragged) att_mask(s0, key0 + lastb * ATT_KB + 32, p.T, hf);
     {
         att_scores(s1, kfb, qf[1]);
         att_pv(o1, vfa, pf1);
@@ -403,7 +413,7 @@ __device__ __forceinline__ void att_pass(const AttnArgs &p, const AttLoader &ld,
         att_read_v(vfb, slot(lastb) + ATT_TILE, 1, lq, hf);
         att_sm_end<FAST>(o0, l0, r);
     }
-    if (ragged) att_mask(s1, lastb * ATT_KB + 32, p.T, hf);
+    if (ragged) att_mask(s1, key0 + lastb * ATT_KB + 32, p.T, hf);
     {
         att_pv(o0, vfb, pf0);
         const float r = att_sm<FAST>(s1, m1, l1, pf1, c);
@@ -424,20 +434,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lq = lane & 31, hf = lane >> 5;
 
-    // XCD-aware order: consecutive workgroup ids go to different XCDs
-    // (round-robin over 8); remap so that each XCD runs a contiguous range of
-    // (query block, head, batch) work items, i.e. the query blocks of few
-    // heads at a time, which share K and V^T in that XCD's L2.
-    int qblk, h, b;
+    // Work item (query block, head, batch) and key-block range.  Workgroup ids
+    // go to the XCDs round-robin (over 8); each range of workgroups (the whole
+    // items, then the tail chunks) is remapped so that each XCD runs a
+    // contiguous range of it: the query blocks of few heads at a time, which
+    // share K and V^T in that XCD's L2.  Tail chunks are ordered chunk-major.
+    int item, kb0 = 0, nkb = p.nkb, tail = -1;
     {
-        const int nq = gridDim.x, nw = gridDim.x * gridDim.y * gridDim.z;
-        const int lin = blockIdx.x + nq * (blockIdx.y + gridDim.y * blockIdx.z);
+        int lin = blockIdx.x, nw = p.nfull;
+        if (lin >= p.nfull) {
+            lin -= p.nfull;
+            nw = p.ntail * p.nsplit;
+        }
         const int xcd = lin & 7, base = nw >> 3, rem = nw & 7;
         const int w = xcd * base + (xcd < rem ? xcd : rem) + (lin >> 3);
-        qblk = w % nq;
-        h = (w / nq) % gridDim.y;
-        b = w / (nq * gridDim.y);
+        if (blockIdx.x < (unsigned)p.nfull) {
+            item = w;
+        } else {
+            const int chunk = w / p.ntail, ti = w % p.ntail;
+            item = p.nfull + ti;
+            kb0 = chunk * p.kbc;
+            nkb = p.nkb - kb0 < p.kbc ? p.nkb - kb0 : p.kbc;
+            tail = ti * p.nsplit + chunk;
+        }
     }
+    const int qblk = item % p.nq, h = (item / p.nq) % p.H, b = item / (p.nq * p.H);
     const int q0 = qblk * ATT_BQ + wave * 64;
 
     // Q^T operands: lane (q, hf) holds d [16j + 8hf, +8) of query q0 + 32t + q.
@@ -463,8 +484,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
     const AttLoader ld = att_loader(p, b, h, wave, lane);
     f32x16a_t o0[4], o1[4];
-    float l0, l1;
-    att_pass<true>(p, ld, lds, qf, wave, lq, hf, o0, o1, l0, l1);
+    float m0, m1, l0, l1;
+    att_pass<true>(p, ld, lds, qf, wave, lq, hf, kb0, nkb, o0, o1, m0, m1, l0, l1);
     // Rerun the whole workgroup in the safe form when any wave's sums left
     // the range the fixed reference max guarantees (scores that grew by more
     // than ~64 in log2 units past their first sub-block's max).
@@ -472,7 +493,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const bool bad = !(l0 < ATT_FAST_LMAX && l1 < ATT_FAST_LMAX);
     if (__builtin_amdgcn_ballot_w64(bad) && lane == 0) redo[wave] = 1;
     __syncthreads();
-    if (redo[0] | redo[1] | redo[2] | redo[3]) att_pass<false>(p, ld, lds, qf, wave, lq, hf, o0, o1, l0, l1);
+    if (redo[0] | redo[1] | redo[2] | redo[3])
+        att_pass<false>(p, ld, lds, qf, wave, lq, hf, kb0, nkb, o0, o1, m0, m1, l0, l1);
+
+    if (tail >= 0) {
+        // A chunk: unnormalised O^T rows (fp32) and (m, l) of each query, for
+        // k_attn_merge.  Rows [256 queries] x [128 d] per chunk.
+        float *po = p.part_o + (int64_t)tail * (ATT_BQ * ATT_D);
+        float *pml = p.part_ml + (int64_t)tail * (ATT_BQ * 2);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const f32x16a_t(&o)[4] = t ? o1 : o0;
+            const float lf = t ? l1 : l0;
+            const float lt = lf + __shfl_xor(lf, 32, 64);
+            const int ql = wave * 64 + 32 * t + lq;
+            float *prow = po + ql * ATT_D;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int d = 32 * dt + 8 * g + 4 * hf;
+                    *reinterpret_cast<float4 *>(prow + d) =
+                        make_float4(o[dt][4 * g + 0], o[dt][4 * g + 1], o[dt][4 * g + 2], o[dt][4 * g + 3]);
+                }
+            if (hf == 0) *reinterpret_cast<float2 *>(pml + 2 * ql) = make_float2(t ? m1 : m0, lt);
+        }
+        return;
+    }
 
     // O = O^T / l: lane (q, hf) holds dims 32dt + 8(i/4) + 4hf + i%4 of its query.
 #pragma unroll
@@ -496,26 +543,116 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
 }
 
+// Combine the chunks of each tail item: O = sum_c 2^(m_c - M) O_c /
+// sum_c 2^(m_c - M) l_c, M = max_c m_c.  One thread per (item, query, 8 d).
+__global__ __launch_bounds__(256) void k_attn_merge(AttnArgs p) {
+    const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int dg = (int)(g & 15), ql = (int)((g >> 4) & (ATT_BQ - 1));
+    const int ti = (int)(g >> 12);  // 16 x 256 threads per item
+    if (ti >= p.ntail) return;
+    const int item = p.nfull + ti;
+    const int qblk = item % p.nq, h = (item / p.nq) % p.H, b = item / (p.nq * p.H);
+    const int qi = qblk * ATT_BQ + ql;
+    if (qi >= p.S) return;
+    const int nc = p.nsplit;
+    float M = -__builtin_inff();
+    for (int c = 0; c < nc; ++c) {
+        const float m = p.part_ml[((int64_t)(ti * p.nsplit + c) * ATT_BQ + ql) * 2];
+        M = m > M ? m : M;
+    }
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, lsum = 0.f;
+    for (int c = 0; c < nc; ++c) {
+        const int64_t tc = (int64_t)(ti * p.nsplit + c);
+        const float2 ml = *reinterpret_cast<const float2 *>(p.part_ml + (tc * ATT_BQ + ql) * 2);
+        const float w = __builtin_amdgcn_exp2f(ml.x - M);
+        lsum += w * ml.y;
+        const float *src = p.part_o + (tc * ATT_BQ + ql) * ATT_D + dg * 8;
+        const float4 a = *reinterpret_cast<const float4 *>(src), bb = *reinterpret_cast<const float4 *>(src + 4);
+        acc[0] += w * a.x; acc[1] += w * a.y; acc[2] += w * a.z; acc[3] += w * a.w;
+        acc[4] += w * bb.x; acc[5] += w * bb.y; acc[6] += w * bb.z; acc[7] += w * bb.w;
+    }
+    const float inv = 1.0f / lsum;
+    uint16_t *orow = p.o + ((int64_t)b * p.S + qi) * p.ldo + (int64_t)h * ATT_D + dg * 8;
+    // 8-byte stores: ldo need only be a multiple of 4 elements.
+    *reinterpret_cast<uint2 *>(orow) = make_uint2(pack_bf16x2(acc[0] * inv, acc[1] * inv),
+                                                  pack_bf16x2(acc[2] * inv, acc[3] * inv));
+    *reinterpret_cast<uint2 *>(orow + 4) = make_uint2(pack_bf16x2(acc[4] * inv, acc[5] * inv),
+                                                      pack_bf16x2(acc[6] * inv, acc[7] * inv));
+}
+
 }  // namespace qim
 
 using namespace qim;
 
+// Work split.  Every workgroup of k_attn_fwd runs for about the same time and
+// one fits per CU, so W whole items take ceil(W / CUs) rounds; when the last
+// round is partial, its items may run instead as chunks of kbc key blocks plus
+// a merge pass.  Cost model, in units of one workgroup's time per 64-key
+// block (measured ~1.75 us at 24 heads): whole rounds * nkb + chunk rounds *
+// kbc + the partials' HBM traffic (written once, read once by the merge, at
+// ~5 TB/s) + ~3 for the merge launch.  A split is taken when it saves >= 5 %;
+// chunks have at least ATT_MIN_CHUNK blocks.  (At S = T = 4352 and 24 heads
+// the partials' traffic eats the gain of filling the last round, and no split
+// is made; at S = T = 16640 ten chunks per tail item save ~12 %.)
+constexpr int ATT_MIN_CHUNK = 8;
+
+struct AttPlan {
+    int64_t nfull, ntail, nsplit, kbc;
+    int64_t vt_bytes, part_o_bytes, part_ml_bytes;
+    int64_t total() const { return vt_bytes + part_o_bytes + part_ml_bytes; }
+};
+
+static AttPlan att_plan(int64_t B, int64_t S, int64_t T, int64_t H) {
+    const int64_t nq = (S + ATT_BQ - 1) / ATT_BQ, nkb = (T + ATT_KB - 1) / ATT_KB, W = B * H * nq;
+    const int64_t C = device_cus() > 0 ? device_cus() : 256;
+    AttPlan pl{W, 0, 1, nkb, B * H * nkb * ATT_TILE, 0, 0};
+    const int64_t R = W / C, Wr = W - R * C;
+    if (Wr == 0) return pl;
+    const double per_chunk_bytes = 2.0 * (ATT_BQ * ATT_D * 4 + ATT_BQ * 2 * 4);  // written + read
+    const double bytes_per_block = 5e12 * 1.75e-6;
+    double best = 0.95 * (double)((R + 1) * nkb);
+    for (int64_t k = 2; k <= 16; ++k) {
+        const int64_t kbc = (nkb + k - 1) / k;
+        if (kbc < ATT_MIN_CHUNK) break;
+        const int64_t keff = (nkb + kbc - 1) / kbc;
+        const int64_t rounds = (Wr * keff + C - 1) / C;
+        const double cost = (double)(R * nkb + rounds * kbc) + (double)(Wr * keff) * per_chunk_bytes / bytes_per_block + 3.0;
+        if (cost < best) {
+            best = cost;
+            pl.nfull = R * C;
+            pl.ntail = Wr;
+            pl.nsplit = keff;
+            pl.kbc = kbc;
+        }
+    }
+    if (pl.ntail) {
+        pl.part_o_bytes = pl.ntail * pl.nsplit * ATT_BQ * ATT_D * 4;
+        pl.part_ml_bytes = pl.ntail * pl.nsplit * ATT_BQ * 2 * 4;
+    }
+    return pl;
+}
+
 extern "C" int qim_attention(const void *q, int64_t ldq, const void *k, int64_t ldk, const void *v, int64_t ldv,
-                             void *o, int64_t ldo, void *vt_workspace, int64_t B, int64_t S, int64_t T, int64_t H,
-                             int64_t D, float scale, void *stream) {
-    QIM_REQUIRE(q && k && v && o && vt_workspace, QIM_ERR_ARG, "qim_attention: null pointer");
+                             void *o, int64_t ldo, void *workspace, int64_t workspace_bytes, int64_t B, int64_t S,
+                             int64_t T, int64_t H, int64_t D, float scale, void *stream) {
+    QIM_REQUIRE(q && k && v && o && workspace, QIM_ERR_ARG, "qim_attention: null pointer");
     QIM_REQUIRE(D == ATT_D, QIM_ERR_SHAPE, "qim_attention: head dim %lld (128 only)", (long long)D);
     QIM_REQUIRE(scale > 0.0f && scale < 1e30f, QIM_ERR_ARG, "qim_attention: scale must be positive and finite");
     QIM_REQUIRE(B > 0 && S > 0 && T > 0 && H > 0, QIM_ERR_SHAPE, "qim_attention: empty problem");
-    QIM_REQUIRE(B < 65536 && H < 65536 && S < (1 << 30) && T < (1 << 30), QIM_ERR_SHAPE, "qim_attention: too large");
+    QIM_REQUIRE(B < 65536 && H < 65536 && S < (1 << 30) && T < (1 << 30) && B * H * ((S + ATT_BQ - 1) / ATT_BQ) < (1 << 30),
+                QIM_ERR_SHAPE, "qim_attention: too large");
     QIM_REQUIRE(ldq >= H * D && ldk >= H * D && ldv >= H * D && ldo >= H * D && ldq % 8 == 0 && ldk % 8 == 0 &&
                     ldv % 8 == 0 && ldo % 4 == 0,
                 QIM_ERR_LAYOUT, "qim_attention: token strides must cover H*D and be multiples of 8 (ldo: 4)");
-    QIM_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(vt_workspace) &&
+    QIM_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(workspace) &&
                     (reinterpret_cast<uintptr_t>(o) & 7u) == 0,
                 QIM_ERR_LAYOUT, "qim_attention: q, k, v, workspace 16-byte aligned, o 8-byte aligned");
     const int64_t nkb = (T + ATT_KB - 1) / ATT_KB;
     QIM_REQUIRE(B * T * ldk < (1ll << 31), QIM_ERR_SHAPE, "qim_attention: K above 4 GiB of offsets");
+    const AttPlan pl = att_plan(B, S, T, H);
+    QIM_REQUIRE(workspace_bytes >= pl.total(), QIM_ERR_ARG,
+                "qim_attention: workspace of %lld bytes, this problem needs %lld (qim_attention_workspace_bytes)",
+                (long long)workspace_bytes, (long long)pl.total());
     static bool configured = false;
     if (!configured) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_attn_fwd),
@@ -526,16 +663,39 @@ extern "C" int qim_attention(const void *q, int64_t ldq, const void *k, int64_t 
         configured = true;
     }
     hipStream_t st = as_stream(stream);
+    uint8_t *ws = static_cast<uint8_t *>(workspace);
     hipLaunchKernelGGL(k_attn_vt, dim3((unsigned)nkb, (unsigned)H, (unsigned)B), dim3(256), 0, st,
-                       (const uint16_t *)v, ldv, (uint16_t *)vt_workspace, (int)T, (int)H, (int)nkb);
-    AttnArgs a{(const uint16_t *)q, (const uint16_t *)k, (const uint16_t *)vt_workspace, (uint16_t *)o, ldq, ldk, ldo,
-               (int)S, (int)T, (int)H, (int)nkb, scale * 1.4426950408889634f};
-    hipLaunchKernelGGL(k_attn_fwd, dim3((unsigned)((S + ATT_BQ - 1) / ATT_BQ), (unsigned)H, (unsigned)B), dim3(256),
-                       ATT_LDS, st, a);
+                       (const uint16_t *)v, ldv, (uint16_t *)ws, (int)T, (int)H, (int)nkb);
+    AttnArgs a{};
+    a.q = (const uint16_t *)q;
+    a.k = (const uint16_t *)k;
+    a.vt = (const uint16_t *)ws;
+    a.o = (uint16_t *)o;
+    a.ldq = ldq;
+    a.ldk = ldk;
+    a.ldo = ldo;
+    a.S = (int)S;
+    a.T = (int)T;
+    a.H = (int)H;
+    a.nkb = (int)nkb;
+    a.nq = (int)((S + ATT_BQ - 1) / ATT_BQ);
+    a.nfull = (int)pl.nfull;
+    a.ntail = (int)pl.ntail;
+    a.nsplit = (int)pl.nsplit;
+    a.kbc = (int)pl.kbc;
+    a.part_o = reinterpret_cast<float *>(ws + pl.vt_bytes);
+    a.part_ml = reinterpret_cast<float *>(ws + pl.vt_bytes + pl.part_o_bytes);
+    a.scale_log2e = scale * 1.4426950408889634f;
+    const int64_t nwg = pl.nfull + pl.ntail * pl.nsplit;
+    hipLaunchKernelGGL(k_attn_fwd, dim3((unsigned)nwg), dim3(256), ATT_LDS, st, a);
+    if (pl.ntail) {
+        const int64_t threads = pl.ntail * ATT_BQ * (ATT_D / 8);
+        hipLaunchKernelGGL(k_attn_merge, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, a);
+    }
     return check_launch("qim_attention");
 }
 
-extern "C" int64_t qim_attention_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D) {
-    if (B <= 0 || T <= 0 || H <= 0 || D != ATT_D) return 0;
-    return B * H * ((T + ATT_KB - 1) / ATT_KB) * ATT_KB * ATT_D * 2;
+extern "C" int64_t qim_attention_workspace_bytes(int64_t B, int64_t S, int64_t T, int64_t H, int64_t D) {
+    if (B <= 0 || S <= 0 || T <= 0 || H <= 0 || D != ATT_D) return 0;
+    return att_plan(B, S, T, H).total();
 }

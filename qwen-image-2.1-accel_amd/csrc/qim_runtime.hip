@@ -171,7 +171,7 @@ extern "C" int qim_debug_mfma_probe(int shape, float *out, void *stream) {
 
 extern "C" const char *qim_last_error(void) { return g_error; }
 
-extern "C" int qim_abi_version(void) { return 2; }
+extern "C" int qim_abi_version(void) { return 3; }
 
 extern "C" int qim_debug_e4m3_encode(const float *x, void *codes, int64_t n, void *stream) {
     QIM_REQUIRE(x && codes && n >= 0, QIM_ERR_ARG, "qim_debug_e4m3_encode: bad arguments");

@@ -65,12 +65,13 @@ def attention(q, k, v, scale=None, out=None):
                                       "expects bf16 (B, N, H, D) tensors with packed heads and token rows")
     if out is None:
         out = torch.empty((b, s, h, d), device=q.device, dtype=torch.bfloat16)
-    nbytes = _native.lib().qim_attention_workspace_bytes(b, t, h, d)
+    with torch.cuda.device(q.device):
+        nbytes = _native.lib().qim_attention_workspace_bytes(b, s, t, h, d)
     if nbytes <= 0:
         raise _native.Unsupported("attention", _native.QIM_ERR_SHAPE, f"head dim {d} (128 only)")
-    ws = torch.empty(nbytes // 2, device=q.device, dtype=torch.bfloat16)
+    ws = torch.empty(nbytes, device=q.device, dtype=torch.uint8)
     _native.call("qim_attention", _native.ptr(q), q.stride(1), _native.ptr(k), k.stride(1), _native.ptr(v),
-                 v.stride(1), _native.ptr(out), out.stride(1), _native.ptr(ws), b, s, t, h, d,
+                 v.stride(1), _native.ptr(out), out.stride(1), _native.ptr(ws), nbytes, b, s, t, h, d,
                  float(scale if scale is not None else d ** -0.5), _native.stream(q.device))
     return out
 

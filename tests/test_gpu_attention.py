@@ -36,8 +36,10 @@ def check(out, ref):
     assert mx < 0.02 * ref.abs().max().item(), mx
 
 
+# (1, 64, 1000, 1), (1, 256, 2000, 4) and (2, 520, 1500, 3) run split over key
+# ranges (2, 4 and 3 chunks, the last one ragged) and merged.
 @pytest.mark.parametrize("b,s,t,h,mag", [(1, 300, 300, 2, 1.0), (2, 256, 333, 3, 1.0), (1, 64, 1000, 1, 1.0),
-                                         (1, 520, 520, 2, 8.0)])
+                                         (1, 520, 520, 2, 8.0), (1, 256, 2000, 4, 1.0), (2, 520, 1500, 3, 4.0)])
 def test_attention_packed(dev, b, s, t, h, mag):
     say("attention", b, s, t, h, mag)
     g = torch.Generator().manual_seed(b * 1000 + s + t + h)
@@ -48,6 +50,23 @@ def test_attention_packed(dev, b, s, t, h, mag):
     out = attention.attention(q, k, v)
     torch.cuda.synchronize()
     check(out, reference(q, k, v, scale))
+
+
+def test_attention_block_shape_with_split_tail(dev):
+    """The 1024^2 block's shape (S = T = 4352, 24 heads), two images, as views
+    of a fused QKV output: 816 work items on 256 CUs, three whole rounds and
+    the last 48 items split into 5 key chunks and merged.  Checked on heads 0,
+    11 and 23 (every query of both images)."""
+    b, s, h = 2, 4352, 24
+    say("attention block shape", b, s, h)
+    g = torch.Generator().manual_seed(4352)
+    qkv = bf16_randn(g, (b, s, 3 * h * 128)).to(dev)
+    q, k, v = (qkv[:, :, i * h * 128:(i + 1) * h * 128].unflatten(-1, (h, 128)) for i in range(3))
+    out = attention.attention(q, k, v)
+    torch.cuda.synchronize()
+    for hh in (0, 11, 23):
+        sl = slice(hh, hh + 1)
+        check(out[:, :, sl], reference(q[:, :, sl], k[:, :, sl], v[:, :, sl], 128 ** -0.5))
 
 
 def test_attention_on_fused_qkv_views(dev):

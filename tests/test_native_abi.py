@@ -39,7 +39,7 @@ def test_single_hip_runtime():
 
 
 def test_abi_version():
-    assert _native.lib().qim_abi_version() == 2
+    assert _native.lib().qim_abi_version() == 3
 
 
 @pytest.mark.parametrize("name,args,code", [
