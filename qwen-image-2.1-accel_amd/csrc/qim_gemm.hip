@@ -351,6 +351,20 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
     }
 #pragma unroll
     for (int half = 0; half < TI / 2; ++half) {
+        // The residual rows of this half's pass 2, loaded before pass 1 so that
+        // their latency overlaps it (rows past M: clamped, not stored).
+        [[maybe_unused]] uint4 rpre[16 / GPI][4];
+        if constexpr (EPI == QIM_EPI_GATED_RESIDUAL) {
+            const int cl = lane % LPR, gl = lane / LPR;
+#pragma unroll
+            for (int it = 0; it < 16 / GPI; ++it)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    int64_t grow = row0 + half * 64 + 4 * (it * GPI + gl) + r;
+                    grow = grow < p.M ? grow : p.M - 1;
+                    rpre[it][r] = ld_nt(p.res + grow * p.N + col0 + cl * 8);
+                }
+        }
         // pass 1
 #pragma unroll
         for (int tl = 0; tl < 2; ++tl) {
@@ -469,7 +483,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
                     if (grow >= p.M) continue;
                     uint4 o = v;
                     if constexpr (EPI == QIM_EPI_GATED_RESIDUAL) {
-                        const uint4 hv = ld_nt(p.res + grow * p.N + col);
+                        const uint4 hv = rpre[it][r];
                         const uint4 gv = *reinterpret_cast<const uint4 *>(p.gate + (grow / p.seq) * p.N + col);
                         float y[8], h[8], gg[8], z[8];
                         unpack8(v, y);
