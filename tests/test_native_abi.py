@@ -65,6 +65,15 @@ def test_abi_version():
     ("qim_mx_quantize_tiled", (16, 128, 1, 100, 16, 16, None), _native.QIM_ERR_SHAPE),
     ("qim_qk_norm_rope_pack", (16, 16, None, None, None, 16, 16, 16, 16, 16, None, 1, 4, 3, 2, 128,
                                256, 1e-6, 1e-6, None), _native.QIM_ERR_ARG),
+    # attention: head dim 64; scale 0; a workspace smaller than the problem needs; misaligned q
+    ("qim_attention", (16, 3072, 16, 3072, 16, 3072, 16, 3072, 16, 1 << 40, 1, 256, 256, 24, 64, 0.1, None),
+     _native.QIM_ERR_SHAPE),
+    ("qim_attention", (16, 3072, 16, 3072, 16, 3072, 16, 3072, 16, 1 << 40, 1, 256, 256, 24, 128, 0.0, None),
+     _native.QIM_ERR_ARG),
+    ("qim_attention", (16, 3072, 16, 3072, 16, 3072, 16, 3072, 16, 1024, 1, 256, 256, 24, 128, 0.1, None),
+     _native.QIM_ERR_ARG),
+    ("qim_attention", (18, 3072, 16, 3072, 16, 3072, 16, 3072, 16, 1 << 40, 1, 256, 256, 24, 128, 0.1, None),
+     _native.QIM_ERR_LAYOUT),
 ])
 def test_argument_checks_return_status(name, args, code):
     """Rejected before any launch: fake (aligned or misaligned) addresses are
@@ -80,3 +89,25 @@ def test_call_raises_unsupported_and_qimerror():
         _native.call("qim_mx_quantize", 16, 128, 1, 100, 16, 16, None)
     with pytest.raises(_native.QimError):
         _native.call("qim_mx_quantize", None, 0, 1, 128, None, None, None)
+
+
+def test_attention_workspace_bytes():
+    """V^T tiles (16 KiB per batch, head and 64-key block), plus, when the last
+    partial round of work items is split over key ranges (the work split only
+    counts CUs: 256 on MI355X, also the value assumed without a GPU),
+    256 x 128 fp32 partial rows and 256 (m, l) pairs per chunk."""
+    lib = _native.lib()
+    vt = lambda b, t, h: b * h * -(-t // 64) * 16384  # noqa: E731
+    part = 256 * 128 * 4 + 256 * 2 * 4
+    assert lib.qim_attention_workspace_bytes(1, 4352, 4352, 24, 64) == 0
+    assert lib.qim_attention_workspace_bytes(0, 4352, 4352, 24, 128) == 0
+    # 408 items on 256 CUs: the partials' traffic would cost what splitting
+    # the last round saves, so no split.
+    assert lib.qim_attention_workspace_bytes(1, 4352, 4352, 24, 128) == vt(1, 4352, 24)
+    # 1560 items: the last 24 run as 10 chunks of 26 key blocks.
+    assert lib.qim_attention_workspace_bytes(1, 16640, 16640, 24, 128) == vt(1, 16640, 24) + 24 * 10 * part
+    # 16 query blocks x 16 heads = 256 items, one whole round: no split
+    assert lib.qim_attention_workspace_bytes(1, 4096, 8192, 16, 128) == vt(1, 8192, 16)
+    for b, s, t, h in [(1, 300, 300, 2), (2, 520, 1500, 3), (1, 8, 20000, 1), (3, 700, 4352, 40)]:
+        n = lib.qim_attention_workspace_bytes(b, s, t, h, 128)
+        assert n >= vt(b, t, h) and (n - vt(b, t, h)) % part == 0
