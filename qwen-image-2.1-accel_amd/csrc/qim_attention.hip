@@ -653,15 +653,9 @@ extern "C" int qim_attention(const void *q, int64_t ldq, const void *k, int64_t 
     QIM_REQUIRE(workspace_bytes >= pl.total(), QIM_ERR_ARG,
                 "qim_attention: workspace of %lld bytes, this problem needs %lld (qim_attention_workspace_bytes)",
                 (long long)workspace_bytes, (long long)pl.total());
-    static bool configured = false;
-    if (!configured) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_attn_fwd),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, ATT_LDS);
-        if (e != hipSuccess)
-            return fail(QIM_ERR_LAUNCH, "qim_attention: cannot reserve %d bytes of LDS: %s", ATT_LDS,
-                        hipGetErrorString(e));
-        configured = true;
-    }
+    static bool configured[QIM_MAX_DEVICES] = {};
+    if (const int rc = reserve_lds(reinterpret_cast<const void *>(&k_attn_fwd), ATT_LDS, configured, "qim_attention"))
+        return rc;
     hipStream_t st = as_stream(stream);
     uint8_t *ws = static_cast<uint8_t *>(workspace);
     hipLaunchKernelGGL(k_attn_vt, dim3((unsigned)nkb, (unsigned)H, (unsigned)B), dim3(256), 0, st,

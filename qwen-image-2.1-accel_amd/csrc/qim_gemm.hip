@@ -693,15 +693,10 @@ static int64_t main_tile_count(int64_t tiles) {
 
 template <int EPI>
 static int launch_gemm(const GemmArgs &a, int64_t tiles, hipStream_t st) {
-    static bool configured = false;
-    if (!configured) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_mx_gemm<EPI>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES);
-        if (e != hipSuccess)
-            return fail(QIM_ERR_LAUNCH, "qim_mxfp8_gemm: cannot reserve %d bytes of LDS: %s", LDS_BYTES,
-                        hipGetErrorString(e));
-        configured = true;
-    }
+    static bool configured[QIM_MAX_DEVICES] = {};
+    if (const int rc = reserve_lds(reinterpret_cast<const void *>(&k_mx_gemm<EPI>), LDS_BYTES, configured,
+                                   "qim_mxfp8_gemm"))
+        return rc;
     const int64_t grid = a.main_tiles + 4 * (tiles - a.main_tiles);
     hipLaunchKernelGGL(k_mx_gemm<EPI>, dim3((unsigned)grid), dim3(256), LDS_BYTES, st, a);
     return QIM_OK;

@@ -25,14 +25,25 @@ int check_launch(const char *what) {
 }
 
 int device_cus() {
-    static int cached[64] = {0};
+    static int cached[QIM_MAX_DEVICES] = {0};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
-    if (dev < 64 && cached[dev]) return cached[dev];
+    if (dev < QIM_MAX_DEVICES && cached[dev]) return cached[dev];
     int n = 0;
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    if (dev < 64) cached[dev] = n;
+    if (dev < QIM_MAX_DEVICES) cached[dev] = n;
     return n;
+}
+
+int reserve_lds(const void *fn, int bytes, bool (&done)[QIM_MAX_DEVICES], const char *who) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return fail(QIM_ERR_LAUNCH, "%s: no current device", who);
+    if (dev < QIM_MAX_DEVICES && done[dev]) return QIM_OK;
+    const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e != hipSuccess)
+        return fail(QIM_ERR_LAUNCH, "%s: cannot reserve %d bytes of LDS: %s", who, bytes, hipGetErrorString(e));
+    if (dev < QIM_MAX_DEVICES) done[dev] = true;
+    return QIM_OK;
 }
 
 // ----------------------------------------------------------- test hooks ----
