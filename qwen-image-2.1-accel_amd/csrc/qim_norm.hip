@@ -53,7 +53,10 @@ constexpr uint32_t BF16X2_NEG_ZERO = 0x80008000u, BF16X2_ONE = 0x3f803f80u;
 // branches; otherwise lanes past the row end hold zeros (any D % 8 == 0).
 // Two waves of three vectors per lane was the fastest split of config 1
 // measured on MI355X.
-template <bool QUANT, int NV, bool FULL>
+// RG: the call has a residual or a gate.  Without them (the block's
+// LN * (1 + scale) + shift) the kernel skips their loads, registers and
+// arithmetic: with gate 1 and residual -0 those steps return t3 unchanged.
+template <bool QUANT, int NV, bool FULL, bool RG>
 __global__ __launch_bounds__(FULL ? 64 * ADALN_FULL_WAVES : 64 * ADALN_MAX_WAVES) void k_adaln(AdaLNArgs p) {
     __shared__ double red[2][FULL ? ADALN_FULL_WAVES : ADALN_MAX_WAVES];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -89,7 +92,7 @@ __global__ __launch_bounds__(FULL ? 64 * ADALN_FULL_WAVES : 64 * ADALN_MAX_WAVES
         xv[i] = ok ? ld_nt(xr + j) : zero;
         sv[i] = ok ? sc[j] : zero;
     }
-    if (p.res) {
+    if (RG && p.res) {
         const uint4 *rr = reinterpret_cast<const uint4 *>(p.res + row * p.D);
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
@@ -111,7 +114,7 @@ __global__ __launch_bounds__(FULL ? 64 * ADALN_FULL_WAVES : 64 * ADALN_MAX_WAVES
 #pragma unroll
         for (int i = 0; i < NV; ++i) hv[i] = neg0;
     }
-    if (p.gate) {
+    if (RG && p.gate) {
         const uint4 *ga = reinterpret_cast<const uint4 *>(p.gate + (int64_t)b * p.D);
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
@@ -168,8 +171,10 @@ __global__ __launch_bounds__(FULL ? 64 * ADALN_FULL_WAVES : 64 * ADALN_MAX_WAVES
         float sf[8], hf[8], gf[8], rf[8], o[8];
         unpack8(sv[i], sf);
         unpack8(hv[i], hf);
-        unpack8(gv[i], gf);
-        unpack8(rv[i], rf);
+        if constexpr (RG) {
+            unpack8(gv[i], gf);
+            unpack8(rv[i], rf);
+        }
 #pragma unroll
         for (int t = 0; t < 8; t += 2) {
             float a0 = (x[i][t] - mean) * rstd, a1 = (x[i][t + 1] - mean) * rstd;
@@ -182,19 +187,26 @@ __global__ __launch_bounds__(FULL ? 64 * ADALN_FULL_WAVES : 64 * ADALN_MAX_WAVES
             a0 += hf[t];
             a1 += hf[t + 1];
             rbf2(a0, a1);                                             // t3
-            a0 *= gf[t];
-            a1 *= gf[t + 1];
-            rbf2(a0, a1);                                             // t4
-            o[t] = rf[t] + a0;
-            o[t + 1] = rf[t + 1] + a1;
+            if constexpr (RG) {
+                a0 *= gf[t];
+                a1 *= gf[t + 1];
+                rbf2(a0, a1);                                         // t4
+                o[t] = rf[t] + a0;
+                o[t + 1] = rf[t + 1] + a1;
+            } else {
+                o[t] = a0;
+                o[t + 1] = a1;
+            }
         }
         if constexpr (!QUANT) {
             st_nt(reinterpret_cast<uint4 *>(p.out + row * p.D) + j, pack8(o));
         } else {
-            rbf2(o[0], o[1]);
-            rbf2(o[2], o[3]);
-            rbf2(o[4], o[5]);
-            rbf2(o[6], o[7]);
+            if constexpr (RG) {
+                rbf2(o[0], o[1]);
+                rbf2(o[2], o[3]);
+                rbf2(o[4], o[5]);
+                rbf2(o[6], o[7]);
+            }
             // A 32-element block is 4 adjacent lanes; 4 adjacent blocks (16
             // lanes) own one dword of the swizzled scale array.
             const uint32_t m = group_umax<4>(absmax_bits8(o));
@@ -219,34 +231,39 @@ __global__ __launch_bounds__(FULL ? 64 * ADALN_FULL_WAVES : 64 * ADALN_MAX_WAVES
 // Picks the split of a row: full coverage with NV in {3, 4, 2, 1} vectors per
 // lane (the first that divides D/8 into at most 4 whole waves; D = 3072: 3 x 2,
 // D = 4096: 4 x 2), else the masked kernel with 2 vectors per lane.
-template <bool QUANT>
-static int launch_adaln(const AdaLNArgs &a, hipStream_t st) {
+template <bool QUANT, bool RG>
+static int launch_adaln_rg(const AdaLNArgs &a, hipStream_t st) {
     const int nvec = a.D / 8;
     if (a.rows_pad >= (1ll << 31) || a.seq >= (1ll << 31)) return fail(QIM_ERR_SHAPE, "adaln: too many rows");
     const dim3 grid((unsigned)a.rows_pad);
     if (nvec % 64 == 0) {
         const int k = nvec / 64;
         if (k % 3 == 0 && k / 3 <= ADALN_FULL_WAVES) {
-            hipLaunchKernelGGL((k_adaln<QUANT, 3, true>), grid, dim3(64 * (k / 3)), 0, st, a);
+            hipLaunchKernelGGL((k_adaln<QUANT, 3, true, RG>), grid, dim3(64 * (k / 3)), 0, st, a);
             return QIM_OK;
         }
         if (k % 4 == 0 && k / 4 <= ADALN_FULL_WAVES) {
-            hipLaunchKernelGGL((k_adaln<QUANT, 4, true>), grid, dim3(64 * (k / 4)), 0, st, a);
+            hipLaunchKernelGGL((k_adaln<QUANT, 4, true, RG>), grid, dim3(64 * (k / 4)), 0, st, a);
             return QIM_OK;
         }
         if (k % 2 == 0 && k / 2 <= ADALN_FULL_WAVES) {
-            hipLaunchKernelGGL((k_adaln<QUANT, 2, true>), grid, dim3(64 * (k / 2)), 0, st, a);
+            hipLaunchKernelGGL((k_adaln<QUANT, 2, true, RG>), grid, dim3(64 * (k / 2)), 0, st, a);
             return QIM_OK;
         }
         if (k <= ADALN_FULL_WAVES) {
-            hipLaunchKernelGGL((k_adaln<QUANT, 1, true>), grid, dim3(64 * k), 0, st, a);
+            hipLaunchKernelGGL((k_adaln<QUANT, 1, true, RG>), grid, dim3(64 * k), 0, st, a);
             return QIM_OK;
         }
     }
     const int waves = (nvec + 127) / 128;
     if (waves > ADALN_MAX_WAVES) return fail(QIM_ERR_SHAPE, "adaln: D=%d exceeds %d", a.D, 8 * 128 * ADALN_MAX_WAVES);
-    hipLaunchKernelGGL((k_adaln<QUANT, 2, false>), grid, dim3(64 * waves), 0, st, a);
+    hipLaunchKernelGGL((k_adaln<QUANT, 2, false, RG>), grid, dim3(64 * waves), 0, st, a);
     return QIM_OK;
+}
+
+template <bool QUANT>
+static int launch_adaln(const AdaLNArgs &a, hipStream_t st) {
+    return (a.res || a.gate) ? launch_adaln_rg<QUANT, true>(a, st) : launch_adaln_rg<QUANT, false>(a, st);
 }
 
 // ---------------------------------------------------- RMSNorm + RoPE ----
