@@ -48,11 +48,12 @@ struct AttnArgs {
     int nq;                 // query blocks per (batch, head)
     // Work split (att_plan): workgroups [0, nfull) each run one whole work item
     // (query block, head, batch); the remaining ntail items run as nsplit
-    // chunks of kbc key blocks each, writing partial results (part_o: fp32
-    // unnormalised O^T rows, part_ml: (m, l) per query) that k_attn_merge
-    // combines.
+    // chunks of kbc key blocks each, writing partial results (part_o: each
+    // chunk's normalised output rows O_c / l_c in bf16, part_ml: (m, l) per
+    // query in fp32) that k_attn_merge combines.
     int nfull, ntail, nsplit, kbc;
-    float *part_o, *part_ml;
+    uint16_t *part_o;
+    float *part_ml;
     float scale_log2e;
 };
 
@@ -496,32 +497,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     if (redo[0] | redo[1] | redo[2] | redo[3])
         att_pass<false>(p, ld, lds, qf, wave, lq, hf, kb0, nkb, o0, o1, m0, m1, l0, l1);
 
-    if (tail >= 0) {
-        // A chunk: unnormalised O^T rows (fp32) and (m, l) of each query, for
-        // k_attn_merge.  Rows [256 queries] x [128 d] per chunk.
-        float *po = p.part_o + (int64_t)tail * (ATT_BQ * ATT_D);
-        float *pml = p.part_ml + (int64_t)tail * (ATT_BQ * 2);
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const f32x16a_t(&o)[4] = t ? o1 : o0;
-            const float lf = t ? l1 : l0;
-            const float lt = lf + __shfl_xor(lf, 32, 64);
-            const int ql = wave * 64 + 32 * t + lq;
-            float *prow = po + ql * ATT_D;
-#pragma unroll
-            for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const int d = 32 * dt + 8 * g + 4 * hf;
-                    *reinterpret_cast<float4 *>(prow + d) =
-                        make_float4(o[dt][4 * g + 0], o[dt][4 * g + 1], o[dt][4 * g + 2], o[dt][4 * g + 3]);
-                }
-            if (hf == 0) *reinterpret_cast<float2 *>(pml + 2 * ql) = make_float2(t ? m1 : m0, lt);
-        }
-        return;
-    }
-
     // O = O^T / l: lane (q, hf) holds dims 32dt + 8(i/4) + 4hf + i%4 of its query.
+    // A tail chunk writes the same bf16 rows into its part_o slot (256 x 128)
+    // and (m, l) of each query into part_ml, for k_attn_merge.
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
         const f32x16a_t(&o)[4] = t ? o1 : o0;
@@ -531,6 +509,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         const int qi = q0 + 32 * t + lq;
         if (qi >= p.S) continue;
         uint16_t *orow = p.o + ((int64_t)b * p.S + qi) * p.ldo + (int64_t)h * ATT_D;
+        if (tail >= 0) {
+            const int ql = wave * 64 + 32 * t + lq;
+            orow = p.part_o + ((int64_t)tail * ATT_BQ + ql) * ATT_D;
+            if (hf == 0)
+                *reinterpret_cast<float2 *>(p.part_ml + ((int64_t)tail * ATT_BQ + ql) * 2) =
+                    make_float2(t ? m1 : m0, lt);
+        }
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
@@ -543,8 +528,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
 }
 
-// Combine the chunks of each tail item: O = sum_c 2^(m_c - M) O_c /
-// sum_c 2^(m_c - M) l_c, M = max_c m_c.  One thread per (item, query, 8 d).
+// Combine the chunks of each tail item from their normalised rows
+// R_c = O_c / l_c: O = sum_c w_c R_c / sum_c w_c with w_c = 2^(m_c - M) l_c,
+// M = max_c m_c.  One thread per (item, query, 8 d).
 __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs p) {
     const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int dg = (int)(g & 15), ql = (int)((g >> 4) & (ATT_BQ - 1));
@@ -560,18 +546,18 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs p) {
         const float m = p.part_ml[((int64_t)(ti * p.nsplit + c) * ATT_BQ + ql) * 2];
         M = m > M ? m : M;
     }
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, lsum = 0.f;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, wsum = 0.f;
     for (int c = 0; c < nc; ++c) {
         const int64_t tc = (int64_t)(ti * p.nsplit + c);
         const float2 ml = *reinterpret_cast<const float2 *>(p.part_ml + (tc * ATT_BQ + ql) * 2);
-        const float w = __builtin_amdgcn_exp2f(ml.x - M);
-        lsum += w * ml.y;
-        const float *src = p.part_o + (tc * ATT_BQ + ql) * ATT_D + dg * 8;
-        const float4 a = *reinterpret_cast<const float4 *>(src), bb = *reinterpret_cast<const float4 *>(src + 4);
-        acc[0] += w * a.x; acc[1] += w * a.y; acc[2] += w * a.z; acc[3] += w * a.w;
-        acc[4] += w * bb.x; acc[5] += w * bb.y; acc[6] += w * bb.z; acc[7] += w * bb.w;
+        const float w = __builtin_amdgcn_exp2f(ml.x - M) * ml.y;
+        wsum += w;
+        float r[8];
+        unpack8(*reinterpret_cast<const uint4 *>(p.part_o + (tc * ATT_BQ + ql) * ATT_D + dg * 8), r);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] += w * r[e];
     }
-    const float inv = 1.0f / lsum;
+    const float inv = 1.0f / wsum;
     uint16_t *orow = p.o + ((int64_t)b * p.S + qi) * p.ldo + (int64_t)h * ATT_D + dg * 8;
     // 8-byte stores: ldo need only be a multiple of 4 elements.
     *reinterpret_cast<uint2 *>(orow) = make_uint2(pack_bf16x2(acc[0] * inv, acc[1] * inv),
@@ -591,9 +577,10 @@ using namespace qim;
 // block (measured ~1.75 us at 24 heads): whole rounds * nkb + chunk rounds *
 // kbc + the partials' HBM traffic (written once, read once by the merge, at
 // ~5 TB/s) + ~3 for the merge launch.  A split is taken when it saves >= 5 %;
-// chunks have at least ATT_MIN_CHUNK blocks.  (At S = T = 4352 and 24 heads
-// the partials' traffic eats the gain of filling the last round, and no split
-// is made; at S = T = 16640 ten chunks per tail item save ~12 %.)
+// chunks have at least ATT_MIN_CHUNK blocks.  Partials are bf16 rows and
+// fp32 (m, l): 66 KiB per chunk.  (At S = T = 16640 and 24 heads the 24 tail
+// items run as 10 chunks each, ~10 % faster; at S = T = 4352 the 152 tail
+// items of one image run as 3 chunks each, ~1 % faster.)
 constexpr int ATT_MIN_CHUNK = 8;
 
 struct AttPlan {
@@ -608,7 +595,7 @@ static AttPlan att_plan(int64_t B, int64_t S, int64_t T, int64_t H) {
     AttPlan pl{W, 0, 1, nkb, B * H * nkb * ATT_TILE, 0, 0};
     const int64_t R = W / C, Wr = W - R * C;
     if (Wr == 0) return pl;
-    const double per_chunk_bytes = 2.0 * (ATT_BQ * ATT_D * 4 + ATT_BQ * 2 * 4);  // written + read
+    const double per_chunk_bytes = 2.0 * (ATT_BQ * ATT_D * 2 + ATT_BQ * 2 * 4);  // written + read
     const double bytes_per_block = 5e12 * 1.75e-6;
     double best = 0.95 * (double)((R + 1) * nkb);
     for (int64_t k = 2; k <= 16; ++k) {
@@ -626,7 +613,7 @@ static AttPlan att_plan(int64_t B, int64_t S, int64_t T, int64_t H) {
         }
     }
     if (pl.ntail) {
-        pl.part_o_bytes = pl.ntail * pl.nsplit * ATT_BQ * ATT_D * 4;
+        pl.part_o_bytes = pl.ntail * pl.nsplit * ATT_BQ * ATT_D * 2;
         pl.part_ml_bytes = pl.ntail * pl.nsplit * ATT_BQ * 2 * 4;
     }
     return pl;
@@ -677,7 +664,7 @@ extern "C" int qim_attention(const void *q, int64_t ldq, const void *k, int64_t 
     a.ntail = (int)pl.ntail;
     a.nsplit = (int)pl.nsplit;
     a.kbc = (int)pl.kbc;
-    a.part_o = reinterpret_cast<float *>(ws + pl.vt_bytes);
+    a.part_o = reinterpret_cast<uint16_t *>(ws + pl.vt_bytes);
     a.part_ml = reinterpret_cast<float *>(ws + pl.vt_bytes + pl.part_o_bytes);
     a.scale_log2e = scale * 1.4426950408889634f;
     const int64_t nwg = pl.nfull + pl.ntail * pl.nsplit;

@@ -95,15 +95,15 @@ def test_attention_workspace_bytes():
     """V^T tiles (16 KiB per batch, head and 64-key block), plus, when the last
     partial round of work items is split over key ranges (the work split only
     counts CUs: 256 on MI355X, also the value assumed without a GPU),
-    256 x 128 fp32 partial rows and 256 (m, l) pairs per chunk."""
+    256 x 128 bf16 normalised output rows and 256 fp32 (m, l) pairs per chunk."""
     lib = _native.lib()
     vt = lambda b, t, h: b * h * -(-t // 64) * 16384  # noqa: E731
-    part = 256 * 128 * 4 + 256 * 2 * 4
+    part = 256 * 128 * 2 + 256 * 2 * 4
     assert lib.qim_attention_workspace_bytes(1, 4352, 4352, 24, 64) == 0
     assert lib.qim_attention_workspace_bytes(0, 4352, 4352, 24, 128) == 0
-    # 408 items on 256 CUs: the partials' traffic would cost what splitting
-    # the last round saves, so no split.
-    assert lib.qim_attention_workspace_bytes(1, 4352, 4352, 24, 128) == vt(1, 4352, 24)
+    # 408 items on 256 CUs: the last 152 run as 3 chunks of 23 key blocks
+    # (456 chunks, two rounds of a third of an item each).
+    assert lib.qim_attention_workspace_bytes(1, 4352, 4352, 24, 128) == vt(1, 4352, 24) + 152 * 3 * part
     # 1560 items: the last 24 run as 10 chunks of 26 key blocks.
     assert lib.qim_attention_workspace_bytes(1, 16640, 16640, 24, 128) == vt(1, 16640, 24) + 24 * 10 * part
     # 16 query blocks x 16 heads = 256 items, one whole round: no split
