@@ -305,10 +305,10 @@ def bench_block(tokens, steps, warmup, with_attention=False):
     attn = None
     if with_attention:
         from qwen_image_accel.kernels import attention
-        attn = attention.attention
+        attn = attention.attention_mxfp8  # the attention output quantized in the same pass
 
     def step(i):
-        blk.forward(h, mod, freqs, attention_fn=attn)
+        blk.forward(h, mod, freqs, attention_mxfp8_fn=attn)
     us = Timed(step, max(3, steps // 20), warmup).run() * 1e3
     flops = blk.flops(tokens)
     return dict(us=us, flops=flops, tflops=flops / us / 1e6, tokens=tokens,

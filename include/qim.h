@@ -202,6 +202,19 @@ int qim_attention(const void *q, int64_t ldq, const void *k, int64_t ldk, const 
                   int64_t T, int64_t H, int64_t D, float scale, void *stream);
 int64_t qim_attention_workspace_bytes(int64_t B, int64_t S, int64_t T, int64_t H, int64_t D);
 
+/* qim_attention with its output quantized to MXFP8 in the same pass: exactly
+ * the codes and scales qim_mx_quantize (tiled = 0) or qim_mx_quantize_tiled
+ * (tiled = 1) would write for qim_attention's bf16 output viewed as a
+ * (B*S, H*D) matrix, without that matrix: codes (Mp, H*D) E4M3, Mp =
+ * B*S rounded up to 128 (padding rows zero), scales Mp*H*D/32 E8M0 bytes
+ * in the swizzled layout; both 16-byte aligned.  The reference quantizes the
+ * attention output for the MXFP8 out-projection in a separate pass
+ * (optimizations/quantized_decode.py:81-96 with kernels/mxfp8.py:59-67); no
+ * reference entry point fuses the two.  Workspace as for qim_attention. */
+int qim_attention_mxfp8(const void *q, int64_t ldq, const void *k, int64_t ldk, const void *v, int64_t ldv,
+                        void *codes, void *scales, int tiled, void *workspace, int64_t workspace_bytes,
+                        int64_t B, int64_t S, int64_t T, int64_t H, int64_t D, float scale, void *stream);
+
 /* Test hooks: the device conversions every kernel uses, applied elementwise
  * (fp32 -> E4M3 code; fp32 -> bf16 bits), and one scaled MFMA
  * (32x32x64, E4M3 x E4M3) on a single tile: a (32, 64) codes, b (32, 64) codes

@@ -55,7 +55,19 @@ struct AttnArgs {
     uint16_t *part_o;
     float *part_ml;
     float scale_log2e;
+    // MXFP8 output (qim_attention_mxfp8) instead of o: E4M3 codes of the
+    // (B*S, H*128) output, row-major or in the GEMM's tiled layout over Mp
+    // rows (mxt_offset), and its swizzled E8M0 scales.
+    uint8_t *qcodes, *qscales;
+    int64_t Mp;
+    int tiled;
 };
+
+// One query row's 4-column group of an MXFP8 output: code byte offset.
+__device__ __forceinline__ int64_t att_code_offset(const AttnArgs &p, int64_t row, int64_t k) {
+    const int64_t K = (int64_t)p.H * ATT_D;
+    return p.tiled ? mxt_offset(row, k, p.Mp, K) : row * K + k;
+}
 
 // ---------------------------------------------------------- V transpose --
 // One workgroup per (batch, head, key block): 64 keys x 128 d through LDS.
@@ -428,6 +440,7 @@ __device__ __forceinline__ void att_pass(const AttnArgs &p, const AttLoader &ld,
 // every |O| (for |V| < 2^63) stayed finite.
 constexpr float ATT_FAST_LMAX = 18446744073709551616.0f;  // 2^64
 
+template <bool QOUT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_attn_fwd(AttnArgs p) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
     __shared__ int redo[4];
@@ -508,6 +521,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         const float inv = 1.0f / lt;
         const int qi = q0 + 32 * t + lq;
         if (qi >= p.S) continue;
+        if (QOUT && tail < 0) {
+            // MXFP8: the bf16 values the plain output would hold, quantized as
+            // qim_mx_quantize does.  A 32-column block (dt) is this lane's 16
+            // values and its partner's (lane ^ 32).
+            const int64_t row = (int64_t)b * p.S + qi;
+            uint32_t sc = 0;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+                float f[16];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) f[i] = rbf(o[dt][i] * inv);
+                uint32_t m = absmax_bits8(f);
+                const uint32_t m2 = absmax_bits8(f + 8);
+                m = m2 > m ? m2 : m;
+                const uint32_t mp = (uint32_t)__shfl_xor((int)m, 32, 64);
+                m = mp > m ? mp : m;
+                const int e = mx_exponent(__uint_as_float(m));
+                const float ie = mx_inverse(e);
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int64_t k = (int64_t)h * ATT_D + 32 * dt + 8 * g + 4 * hf;
+                    *reinterpret_cast<uint32_t *>(p.qcodes + att_code_offset(p, row, k)) =
+                        cvt_e4m3x4(f[4 * g] * ie, f[4 * g + 1] * ie, f[4 * g + 2] * ie, f[4 * g + 3] * ie);
+                }
+                sc |= (uint32_t)e << (8 * dt);
+            }
+            if (hf == 0)
+                *reinterpret_cast<uint32_t *>(p.qscales + mx_scale_offset(row, 4 * h, (int64_t)p.H * ATT_D)) = sc;
+            continue;
+        }
         uint16_t *orow = p.o + ((int64_t)b * p.S + qi) * p.ldo + (int64_t)h * ATT_D;
         if (tail >= 0) {
             const int ql = wave * 64 + 32 * t + lq;
@@ -558,12 +601,36 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs p) {
         for (int e = 0; e < 8; ++e) acc[e] += w * r[e];
     }
     const float inv = 1.0f / wsum;
+    if (p.qcodes) {
+        // MXFP8 output: a 32-column block is 4 adjacent threads (dg 4j .. 4j+3).
+        float f[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] = rbf(acc[e] * inv);
+        int e;
+        const uint2 c = quantize8(f, e);
+        const int64_t row = (int64_t)b * p.S + qi;
+        *reinterpret_cast<uint2 *>(p.qcodes + att_code_offset(p, row, (int64_t)h * ATT_D + dg * 8)) = c;
+        if ((dg & 3) == 0) p.qscales[mx_scale_offset(row, 4 * h + (dg >> 2), (int64_t)p.H * ATT_D)] = (uint8_t)e;
+        return;
+    }
     uint16_t *orow = p.o + ((int64_t)b * p.S + qi) * p.ldo + (int64_t)h * ATT_D + dg * 8;
     // 8-byte stores: ldo need only be a multiple of 4 elements.
     *reinterpret_cast<uint2 *>(orow) = make_uint2(pack_bf16x2(acc[0] * inv, acc[1] * inv),
                                                   pack_bf16x2(acc[2] * inv, acc[3] * inv));
     *reinterpret_cast<uint2 *>(orow + 4) = make_uint2(pack_bf16x2(acc[4] * inv, acc[5] * inv),
                                                       pack_bf16x2(acc[6] * inv, acc[7] * inv));
+}
+
+// MXFP8 output rows [M, Mp) (the padding of the last 128-row scale block):
+// zero codes and scales, as qim_mx_quantize writes them.  One thread per
+// 16-byte code chunk.
+__global__ __launch_bounds__(256) void k_attn_qpad(AttnArgs p, int64_t M) {
+    const int64_t K = (int64_t)p.H * ATT_D, per_row = K / 16;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t r = M + i / per_row, c = i % per_row;
+    if (r >= p.Mp) return;
+    *reinterpret_cast<uint4 *>(p.qcodes + att_code_offset(p, r, c * 16)) = make_uint4(0, 0, 0, 0);
+    if (c < K / 128) *reinterpret_cast<uint32_t *>(p.qscales + mx_scale_offset(r, 4 * c, K)) = 0;
 }
 
 }  // namespace qim
@@ -619,30 +686,35 @@ static AttPlan att_plan(int64_t B, int64_t S, int64_t T, int64_t H) {
     return pl;
 }
 
-extern "C" int qim_attention(const void *q, int64_t ldq, const void *k, int64_t ldk, const void *v, int64_t ldv,
-                             void *o, int64_t ldo, void *workspace, int64_t workspace_bytes, int64_t B, int64_t S,
-                             int64_t T, int64_t H, int64_t D, float scale, void *stream) {
-    QIM_REQUIRE(q && k && v && o && workspace, QIM_ERR_ARG, "qim_attention: null pointer");
-    QIM_REQUIRE(D == ATT_D, QIM_ERR_SHAPE, "qim_attention: head dim %lld (128 only)", (long long)D);
-    QIM_REQUIRE(scale > 0.0f && scale < 1e30f, QIM_ERR_ARG, "qim_attention: scale must be positive and finite");
-    QIM_REQUIRE(B > 0 && S > 0 && T > 0 && H > 0, QIM_ERR_SHAPE, "qim_attention: empty problem");
+// The checks and launches both entry points share.  Output: bf16 rows of o
+// (ldo elements apart), or MXFP8 codes and scales when qcodes is set.
+static int attention_run(const char *who, const void *q, int64_t ldq, const void *k, int64_t ldk, const void *v,
+                         int64_t ldv, void *o, int64_t ldo, void *qcodes, void *qscales, int tiled, void *workspace,
+                         int64_t workspace_bytes, int64_t B, int64_t S, int64_t T, int64_t H, int64_t D, float scale,
+                         void *stream) {
+    QIM_REQUIRE(q && k && v && (o || (qcodes && qscales)) && workspace, QIM_ERR_ARG, "%s: null pointer", who);
+    QIM_REQUIRE(D == ATT_D, QIM_ERR_SHAPE, "%s: head dim %lld (128 only)", who, (long long)D);
+    QIM_REQUIRE(scale > 0.0f && scale < 1e30f, QIM_ERR_ARG, "%s: scale must be positive and finite", who);
+    QIM_REQUIRE(B > 0 && S > 0 && T > 0 && H > 0, QIM_ERR_SHAPE, "%s: empty problem", who);
     QIM_REQUIRE(B < 65536 && H < 65536 && S < (1 << 30) && T < (1 << 30) && B * H * ((S + ATT_BQ - 1) / ATT_BQ) < (1 << 30),
-                QIM_ERR_SHAPE, "qim_attention: too large");
-    QIM_REQUIRE(ldq >= H * D && ldk >= H * D && ldv >= H * D && ldo >= H * D && ldq % 8 == 0 && ldk % 8 == 0 &&
-                    ldv % 8 == 0 && ldo % 4 == 0,
-                QIM_ERR_LAYOUT, "qim_attention: token strides must cover H*D and be multiples of 8 (ldo: 4)");
+                QIM_ERR_SHAPE, "%s: too large", who);
+    QIM_REQUIRE(ldq >= H * D && ldk >= H * D && ldv >= H * D && ldq % 8 == 0 && ldk % 8 == 0 && ldv % 8 == 0 &&
+                    (qcodes || (ldo >= H * D && ldo % 4 == 0)),
+                QIM_ERR_LAYOUT, "%s: token strides must cover H*D and be multiples of 8 (ldo: 4)", who);
     QIM_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(workspace) &&
-                    (reinterpret_cast<uintptr_t>(o) & 7u) == 0,
-                QIM_ERR_LAYOUT, "qim_attention: q, k, v, workspace 16-byte aligned, o 8-byte aligned");
+                    (qcodes ? aligned16(qcodes) && aligned16(qscales) : (reinterpret_cast<uintptr_t>(o) & 7u) == 0),
+                QIM_ERR_LAYOUT, "%s: q, k, v, workspace (and codes, scales) 16-byte aligned, o 8-byte aligned", who);
+    QIM_REQUIRE(tiled == 0 || tiled == 1, QIM_ERR_ARG, "%s: tiled must be 0 or 1", who);
     const int64_t nkb = (T + ATT_KB - 1) / ATT_KB;
-    QIM_REQUIRE(B * T * ldk < (1ll << 31), QIM_ERR_SHAPE, "qim_attention: K above 4 GiB of offsets");
+    QIM_REQUIRE(B * T * ldk < (1ll << 31), QIM_ERR_SHAPE, "%s: K above 4 GiB of offsets", who);
     const AttPlan pl = att_plan(B, S, T, H);
     QIM_REQUIRE(workspace_bytes >= pl.total(), QIM_ERR_ARG,
-                "qim_attention: workspace of %lld bytes, this problem needs %lld (qim_attention_workspace_bytes)",
+                "%s: workspace of %lld bytes, this problem needs %lld (qim_attention_workspace_bytes)", who,
                 (long long)workspace_bytes, (long long)pl.total());
-    static bool configured[QIM_MAX_DEVICES] = {};
-    if (const int rc = reserve_lds(reinterpret_cast<const void *>(&k_attn_fwd), ATT_LDS, configured, "qim_attention"))
-        return rc;
+    static bool configured[2][QIM_MAX_DEVICES] = {};
+    const void *fwd = qcodes ? reinterpret_cast<const void *>(&k_attn_fwd<true>)
+                             : reinterpret_cast<const void *>(&k_attn_fwd<false>);
+    if (const int rc = reserve_lds(fwd, ATT_LDS, configured[qcodes ? 1 : 0], who)) return rc;
     hipStream_t st = as_stream(stream);
     uint8_t *ws = static_cast<uint8_t *>(workspace);
     hipLaunchKernelGGL(k_attn_vt, dim3((unsigned)nkb, (unsigned)H, (unsigned)B), dim3(256), 0, st,
@@ -667,13 +739,42 @@ extern "C" int qim_attention(const void *q, int64_t ldq, const void *k, int64_t 
     a.part_o = reinterpret_cast<uint16_t *>(ws + pl.vt_bytes);
     a.part_ml = reinterpret_cast<float *>(ws + pl.vt_bytes + pl.part_o_bytes);
     a.scale_log2e = scale * 1.4426950408889634f;
+    const int64_t M = B * S;
+    a.qcodes = static_cast<uint8_t *>(qcodes);
+    a.qscales = static_cast<uint8_t *>(qscales);
+    a.Mp = (M + 127) / 128 * 128;
+    a.tiled = tiled;
     const int64_t nwg = pl.nfull + pl.ntail * pl.nsplit;
-    hipLaunchKernelGGL(k_attn_fwd, dim3((unsigned)nwg), dim3(256), ATT_LDS, st, a);
+    if (qcodes)
+        hipLaunchKernelGGL(k_attn_fwd<true>, dim3((unsigned)nwg), dim3(256), ATT_LDS, st, a);
+    else
+        hipLaunchKernelGGL(k_attn_fwd<false>, dim3((unsigned)nwg), dim3(256), ATT_LDS, st, a);
     if (pl.ntail) {
         const int64_t threads = pl.ntail * ATT_BQ * (ATT_D / 8);
         hipLaunchKernelGGL(k_attn_merge, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, a);
     }
-    return check_launch("qim_attention");
+    if (qcodes && a.Mp > M) {
+        const int64_t threads = (a.Mp - M) * H * ATT_D / 16;
+        hipLaunchKernelGGL(k_attn_qpad, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, a, M);
+    }
+    return check_launch(who);
+}
+
+extern "C" int qim_attention(const void *q, int64_t ldq, const void *k, int64_t ldk, const void *v, int64_t ldv,
+                             void *o, int64_t ldo, void *workspace, int64_t workspace_bytes, int64_t B, int64_t S,
+                             int64_t T, int64_t H, int64_t D, float scale, void *stream) {
+    if (!o) return qim::fail(QIM_ERR_ARG, "qim_attention: null pointer");
+    return attention_run("qim_attention", q, ldq, k, ldk, v, ldv, o, ldo, nullptr, nullptr, 0, workspace,
+                         workspace_bytes, B, S, T, H, D, scale, stream);
+}
+
+extern "C" int qim_attention_mxfp8(const void *q, int64_t ldq, const void *k, int64_t ldk, const void *v,
+                                   int64_t ldv, void *codes, void *scales, int tiled, void *workspace,
+                                   int64_t workspace_bytes, int64_t B, int64_t S, int64_t T, int64_t H, int64_t D,
+                                   float scale, void *stream) {
+    if (!codes || !scales) return qim::fail(QIM_ERR_ARG, "qim_attention_mxfp8: null pointer");
+    return attention_run("qim_attention_mxfp8", q, ldq, k, ldk, v, ldv, nullptr, 0, codes, scales, tiled, workspace,
+                         workspace_bytes, B, S, T, H, D, scale, stream);
 }
 
 extern "C" int64_t qim_attention_workspace_bytes(int64_t B, int64_t S, int64_t T, int64_t H, int64_t D) {

@@ -306,6 +306,19 @@ __device__ __forceinline__ uint32_t group_umax(uint32_t v) {
     return v;
 }
 
+// Quantize one lane's 8 values, which are one quarter of a 32-element block
+// spread over lanes (4j .. 4j+3).  Returns the packed codes; e = exponent.
+__device__ __forceinline__ uint2 quantize8(const float *f, int &e) {
+    uint32_t m = absmax_bits8(f);
+    m = group_umax<4>(m);
+    e = mx_exponent(__uint_as_float(m));
+    float inv = mx_inverse(e);
+    uint2 c;
+    c.x = cvt_e4m3x4(f[0] * inv, f[1] * inv, f[2] * inv, f[3] * inv);
+    c.y = cvt_e4m3x4(f[4] * inv, f[5] * inv, f[6] * inv, f[7] * inv);
+    return c;
+}
+
 // ------------------------------------------------------------- math ----
 
 // SiLU with the reference's rounding: bf16(g / (1 + exp(-g))) with an IEEE

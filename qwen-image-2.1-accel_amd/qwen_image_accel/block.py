@@ -9,8 +9,9 @@ modulation, fused QKV projection, hidden 3072, 24 heads x 128, FFN 12288):
     x   = MXFP8(LN(h) * (1 + scale1) + shift1)             qim_adaln_quantize
     qkv = x @ W_qkv; q,k = rope(RMSNorm(q)), rope(RMSNorm(k))
                                                             qim_mxfp8_gemm_qk_norm_rope
-    o   = attention(q, k, v)        -- out of scope; stand-in o = v
+    o   = attention(q, k, v)        -- qim_attention (attention_fn); stand-in o = v
     h   = h + tanh(g1) * (MXFP8(o) @ W_out)                 qim_mx_quantize + GEMM epilogue
+          (MXFP8(attention(q, k, v)) in one pass:           qim_attention_mxfp8)
     x   = MXFP8(LN(h) * (1 + scale2) + shift2)             qim_adaln_quantize
     a   = MXFP8(silu(x @ W_gate) * (x @ W_up))              GEMM, SwiGLU->MXFP8 epilogue
     h   = h + tanh(g2) * (a @ W_down)                       GEMM, gated-residual epilogue
@@ -81,11 +82,14 @@ class MMDiTBlock:
         return MMDiTBlock.from_weights(w(3 * dim, dim), w(dim, dim), w(ffn, dim), w(ffn, dim),
                                        w(dim, ffn), nq, nk, heads)
 
-    def forward(self, h, modulation, freqs, attention_fn=None):
+    def forward(self, h, modulation, freqs, attention_fn=None, attention_mxfp8_fn=None):
         """h: (B, S, dim) bf16; modulation: (B, 6, dim) bf16 rows
         (shift1, scale1, gate1, shift2, scale2, gate2); freqs: (S, head_dim/2)
         complex64.  ``attention_fn(q, k, v) -> (B, S, dim)`` defaults to the
-        stand-in that returns v."""
+        stand-in that returns v.  ``attention_mxfp8_fn(q, k, v)`` (e.g.
+        ``attention.attention_mxfp8``), when given, returns the attention
+        output already quantized in the tiled layout (the same bytes as
+        quantizing attention_fn's output) and replaces both."""
         b, s, d = h.shape
         shift1, scale1, g1, shift2, scale2, g2 = (modulation[:, i:i + 1] for i in range(6))
         gate1, gate2 = g1.tanh(), g2.tanh()
@@ -99,11 +103,12 @@ class MMDiTBlock:
         qkv4 = qkv.view(b, s, 3 * d)
         q = qkv4[:, :, :d].unflatten(-1, (self.heads, hd))                      # normalised + rotated
         k = qkv4[:, :, d:2 * d].unflatten(-1, (self.heads, hd))
-        if attention_fn is None:
-            o = qkv[:, 2 * d:]                                                   # stand-in: v
+        v = qkv4[:, :, 2 * d:].unflatten(-1, (self.heads, hd))
+        if attention_mxfp8_fn is not None:
+            oq = attention_mxfp8_fn(q, k, v)
         else:
-            o = attention_fn(q, k, qkv4[:, :, 2 * d:].unflatten(-1, (self.heads, hd))).reshape(b * s, d)
-        oq = mxfp8.quantize(o, tiled=True)
+            o = qkv[:, 2 * d:] if attention_fn is None else attention_fn(q, k, v).reshape(b * s, d)  # stand-in: v
+            oq = mxfp8.quantize(o, tiled=True)
         h1 = self._mm(oq, self.w_out, epilogue="gated_residual", gate=gate1.contiguous(),
                       residual=h.reshape(b * s, d), seq=s)
         h1 = h1.view(b, s, d)

@@ -10,6 +10,7 @@ across calls.
 import torch
 
 from qwen_image_accel import _native
+from qwen_image_accel.kernels import mxfp8
 from qwen_image_accel.kernels.bf16 import HEAD_DIMS
 
 
@@ -73,6 +74,33 @@ def attention(q, k, v, scale=None, out=None):
     _native.call("qim_attention", _native.ptr(q), q.stride(1), _native.ptr(k), k.stride(1), _native.ptr(v),
                  v.stride(1), _native.ptr(out), out.stride(1), _native.ptr(ws), nbytes, b, s, t, h, d,
                  float(scale if scale is not None else d ** -0.5), _native.stream(q.device))
+    return out
+
+
+def attention_mxfp8(q, k, v, scale=None, *, tiled=True, out=None):
+    """``mxfp8.quantize(attention(q, k, v).reshape(B*S, H*128), tiled=tiled)``
+    in one pass (libqim's ``qim_attention_mxfp8``): the same codes and scales,
+    without the bf16 output.  The block's out-projection input; the reference
+    runs SDPA and then its quantize kernel (optimizations/quantized_decode.py:
+    70-96).  ``out``: a preallocated ``mxfp8.empty_quantized(B*S, H*128,
+    device, tiled=tiled)``."""
+    b, s, h, d = q.shape
+    t = k.shape[1]
+    for x, n in ((q, s), (k, t), (v, t)):
+        if (x.dtype != torch.bfloat16 or not x.is_cuda or x.shape != (b, n, h, d) or x.stride(3) != 1
+                or x.stride(2) != d or x.stride(0) != n * x.stride(1)):
+            raise _native.Unsupported("attention_mxfp8", _native.QIM_ERR_LAYOUT,
+                                      "expects bf16 (B, N, H, D) tensors with packed heads and token rows")
+    with torch.cuda.device(q.device):
+        nbytes = _native.lib().qim_attention_workspace_bytes(b, s, t, h, d)
+    if nbytes <= 0:
+        raise _native.Unsupported("attention_mxfp8", _native.QIM_ERR_SHAPE, f"head dim {d} (128 only)")
+    if out is None:
+        out = mxfp8.empty_quantized(b * s, h * d, q.device, tiled=tiled)
+    ws = torch.empty(nbytes, device=q.device, dtype=torch.uint8)
+    _native.call("qim_attention_mxfp8", _native.ptr(q), q.stride(1), _native.ptr(k), k.stride(1), _native.ptr(v),
+                 v.stride(1), _native.ptr(out.values), _native.ptr(out.scales), int(tiled), _native.ptr(ws), nbytes,
+                 b, s, t, h, d, float(scale if scale is not None else d ** -0.5), _native.stream(q.device))
     return out
 
 

@@ -11,7 +11,7 @@ and large logits (the running-max subtraction).
 import pytest
 import torch
 
-from qwen_image_accel.kernels import attention
+from qwen_image_accel.kernels import attention, mxfp8
 from tests.helpers import bf16_randn, rel_fro
 
 pytestmark = pytest.mark.gpu
@@ -108,6 +108,30 @@ def test_attention_score_jump_past_first_block(dev, jump):
     ref = reference(q, k, v, scale)
     assert torch.isfinite(out.float()).all()
     check(out, ref)
+
+
+# (2, 200, 333, 3): 400 rows, padded to 512, past the last query block's end;
+# (1, 256, 2000, 4), (2, 520, 1500, 3) and the 4352 shapes run split and merged.
+@pytest.mark.parametrize("b,s,t,h,tiled", [(1, 300, 300, 2, True), (2, 200, 333, 3, False),
+                                           (1, 256, 2000, 4, True), (2, 520, 1500, 3, False),
+                                           (1, 4352, 4352, 24, True), (2, 4352, 4352, 24, True)])
+def test_attention_mxfp8_equals_quantized_output(dev, b, s, t, h, tiled):
+    """The fused MXFP8 output is bit-identical to quantizing the bf16 output
+    (every code and scale byte, padding rows included: the buffers start
+    as 0xff)."""
+    say("attention mxfp8", b, s, t, h, tiled)
+    g = torch.Generator().manual_seed(7 * b + s + t + h)
+    q = bf16_randn(g, (b, s, h, 128)).to(dev)
+    kv = bf16_randn(g, (b, t, 2 * h * 128)).to(dev)
+    k, v = (kv[:, :, i * h * 128:(i + 1) * h * 128].unflatten(-1, (h, 128)) for i in (0, 1))
+    ref = mxfp8.quantize(attention.attention(q, k, v).reshape(b * s, h * 128), tiled=tiled)
+    out = mxfp8.empty_quantized(b * s, h * 128, dev, tiled=tiled)
+    out.values.view(torch.uint8).fill_(0xff)
+    out.scales.view(torch.uint8).fill_(0xff)
+    got = attention.attention_mxfp8(q, k, v, tiled=tiled, out=out)
+    torch.cuda.synchronize()
+    assert torch.equal(got.values.view(torch.uint8), ref.values.view(torch.uint8))
+    assert torch.equal(got.scales.view(torch.uint8), ref.scales.view(torch.uint8))
 
 
 def test_attention_rejects_other_head_dims(dev):

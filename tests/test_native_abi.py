@@ -74,6 +74,13 @@ def test_abi_version():
      _native.QIM_ERR_ARG),
     ("qim_attention", (18, 3072, 16, 3072, 16, 3072, 16, 3072, 16, 1 << 40, 1, 256, 256, 24, 128, 0.1, None),
      _native.QIM_ERR_LAYOUT),
+    # attention_mxfp8: null scales; tiled 2; misaligned codes
+    ("qim_attention_mxfp8", (16, 3072, 16, 3072, 16, 3072, 16, None, 1, 16, 1 << 40, 1, 256, 256, 24, 128, 0.1,
+                             None), _native.QIM_ERR_ARG),
+    ("qim_attention_mxfp8", (16, 3072, 16, 3072, 16, 3072, 16, 16, 2, 16, 1 << 40, 1, 256, 256, 24, 128, 0.1,
+                             None), _native.QIM_ERR_ARG),
+    ("qim_attention_mxfp8", (16, 3072, 16, 3072, 16, 3072, 8, 16, 1, 16, 1 << 40, 1, 256, 256, 24, 128, 0.1,
+                             None), _native.QIM_ERR_LAYOUT),
 ])
 def test_argument_checks_return_status(name, args, code):
     """Rejected before any launch: fake (aligned or misaligned) addresses are
