@@ -302,13 +302,10 @@ def bench_block(tokens, steps, warmup, with_attention=False):
     mod = randn(g, (1, 6, 3072), 0.1)
     freqs = rope.image_table(256, side, side, "cuda")
 
-    attn = None
-    if with_attention:
-        from qwen_image_accel.kernels import attention
-        attn = attention.attention_mxfp8  # the attention output quantized in the same pass
-
     def step(i):
-        blk.forward(h, mod, freqs, attention_mxfp8_fn=attn)
+        # with_attention: the library's attention core, V^T written by the QKV
+        # projection and the output quantized in the same pass
+        blk.forward(h, mod, freqs, fused_attention=with_attention)
     us = Timed(step, max(3, steps // 20), warmup).run() * 1e3
     flops = blk.flops(tokens)
     return dict(us=us, flops=flops, tflops=flops / us / 1e6, tokens=tokens,

@@ -187,6 +187,17 @@ int qim_mxfp8_gemm_qk_norm_rope(const void *aq, const void *as, const void *bq, 
                                 const void *wk, const void *freqs, int64_t seq, float epsq,
                                 float epsk, void *out, int64_t ldo, void *stream);
 
+/* qim_mxfp8_gemm_qk_norm_rope whose V columns leave as the attention core's
+ * V^T tiles instead: written into the first B*H*(seq/64)*16 KiB of a
+ * qim_attention workspace for (B = M / seq, S = T = seq, H), which
+ * qim_attention / qim_attention_mxfp8 then read when passed v = NULL.  The V
+ * columns of out are not written.  seq % 64 == 0, M % seq == 0.  No reference
+ * counterpart: it removes the attention's V transpose pass. */
+int qim_mxfp8_gemm_qk_norm_rope_vt(const void *aq, const void *as, const void *bq, const void *bs,
+                                   int64_t M, int64_t K, int64_t H, int layouts, const void *wq,
+                                   const void *wk, const void *freqs, int64_t seq, float epsq,
+                                   float epsk, void *out, int64_t ldo, void *vt, void *stream);
+
 /* Attention core, the block's softmax(Q K^T * scale) V per (batch, head) over
  * [prefix + target] keys (SDPA in the reference: optimizations/
  * quantized_decode.py:70-77).  q: (B, S, H, D), k, v: (B, T, H, D), o:
@@ -196,7 +207,9 @@ int qim_mxfp8_gemm_qk_norm_rope(const void *aq, const void *as, const void *bq, 
  * workspace: at least qim_attention_workspace_bytes(B, S, T, H, D) bytes,
  * 16-byte aligned, passed with its size (V transposed in 64-key tiles, and
  * the partial results of work items split over key ranges to fill the last
- * round of workgroups; the split depends on the current device's CU count). */
+ * round of workgroups; the split depends on the current device's CU count).
+ * v = NULL (ldv ignored): the workspace already holds V^T, written by
+ * qim_mxfp8_gemm_qk_norm_rope_vt; T % 64 == 0. */
 int qim_attention(const void *q, int64_t ldq, const void *k, int64_t ldk, const void *v, int64_t ldv,
                   void *o, int64_t ldo, void *workspace, int64_t workspace_bytes, int64_t B, int64_t S,
                   int64_t T, int64_t H, int64_t D, float scale, void *stream);

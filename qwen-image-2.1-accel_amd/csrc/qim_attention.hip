@@ -687,18 +687,21 @@ static AttPlan att_plan(int64_t B, int64_t S, int64_t T, int64_t H) {
 }
 
 // The checks and launches both entry points share.  Output: bf16 rows of o
-// (ldo elements apart), or MXFP8 codes and scales when qcodes is set.
+// (ldo elements apart), or MXFP8 codes and scales when qcodes is set.  v null:
+// the workspace already holds V^T (qim_mxfp8_gemm_qk_norm_rope_vt), T % 64 == 0.
 static int attention_run(const char *who, const void *q, int64_t ldq, const void *k, int64_t ldk, const void *v,
                          int64_t ldv, void *o, int64_t ldo, void *qcodes, void *qscales, int tiled, void *workspace,
                          int64_t workspace_bytes, int64_t B, int64_t S, int64_t T, int64_t H, int64_t D, float scale,
                          void *stream) {
-    QIM_REQUIRE(q && k && v && (o || (qcodes && qscales)) && workspace, QIM_ERR_ARG, "%s: null pointer", who);
+    QIM_REQUIRE(q && k && (o || (qcodes && qscales)) && workspace, QIM_ERR_ARG, "%s: null pointer", who);
     QIM_REQUIRE(D == ATT_D, QIM_ERR_SHAPE, "%s: head dim %lld (128 only)", who, (long long)D);
     QIM_REQUIRE(scale > 0.0f && scale < 1e30f, QIM_ERR_ARG, "%s: scale must be positive and finite", who);
     QIM_REQUIRE(B > 0 && S > 0 && T > 0 && H > 0, QIM_ERR_SHAPE, "%s: empty problem", who);
     QIM_REQUIRE(B < 65536 && H < 65536 && S < (1 << 30) && T < (1 << 30) && B * H * ((S + ATT_BQ - 1) / ATT_BQ) < (1 << 30),
                 QIM_ERR_SHAPE, "%s: too large", who);
-    QIM_REQUIRE(ldq >= H * D && ldk >= H * D && ldv >= H * D && ldq % 8 == 0 && ldk % 8 == 0 && ldv % 8 == 0 &&
+    QIM_REQUIRE(v || T % ATT_KB == 0, QIM_ERR_SHAPE, "%s: V^T from the workspace (v null) needs T %% 64 == 0", who);
+    QIM_REQUIRE(ldq >= H * D && ldk >= H * D && (!v || (ldv >= H * D && ldv % 8 == 0)) && ldq % 8 == 0 &&
+                    ldk % 8 == 0 &&
                     (qcodes || (ldo >= H * D && ldo % 4 == 0)),
                 QIM_ERR_LAYOUT, "%s: token strides must cover H*D and be multiples of 8 (ldo: 4)", who);
     QIM_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(workspace) &&
@@ -717,8 +720,9 @@ static int attention_run(const char *who, const void *q, int64_t ldq, const void
     if (const int rc = reserve_lds(fwd, ATT_LDS, configured[qcodes ? 1 : 0], who)) return rc;
     hipStream_t st = as_stream(stream);
     uint8_t *ws = static_cast<uint8_t *>(workspace);
-    hipLaunchKernelGGL(k_attn_vt, dim3((unsigned)nkb, (unsigned)H, (unsigned)B), dim3(256), 0, st,
-                       (const uint16_t *)v, ldv, (uint16_t *)ws, (int)T, (int)H, (int)nkb);
+    if (v)
+        hipLaunchKernelGGL(k_attn_vt, dim3((unsigned)nkb, (unsigned)H, (unsigned)B), dim3(256), 0, st,
+                           (const uint16_t *)v, ldv, (uint16_t *)ws, (int)T, (int)H, (int)nkb);
     AttnArgs a{};
     a.q = (const uint16_t *)q;
     a.k = (const uint16_t *)k;

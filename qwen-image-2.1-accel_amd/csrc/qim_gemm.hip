@@ -61,6 +61,12 @@ struct GemmArgs {
     const float *freqs;
     float epsq, epsk;
     int64_t q_cols, qk_cols;
+    // With vt set, the V columns leave as the attention's V^T tiles instead:
+    // tile (batch, head, key block) of 128 rows (d) x 64 keys at
+    // ((batch * H + head) * vt_nkb + key block) * 8192 elements, vt_nkb =
+    // seq / 64 (seq % 64 == 0).
+    uint16_t *vt;
+    int64_t vt_nkb;
 };
 
 __device__ __forceinline__ int kswz(int row) { return mx_chunk_swizzle(row); }
@@ -344,6 +350,12 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
     uint8_t *reg = lds + wave * (16 * RGS);
     const int64_t col0 = SWI ? gcol0 / 2 : gcol0;  // first output column
     const int64_t F = p.N / 2;
+    // QKV projection with vt: this wave's V columns are staged per column (64
+    // keys, VT_COL bytes apart; the odd stride spreads the pass-1 writes of a
+    // 32-lane group over all banks) and leave as V^T tiles.
+    [[maybe_unused]] constexpr int VT_COL = 136;
+    static_assert(W * VT_COL <= 16 * RGS, "V^T staging fits the wave's region");
+    const bool vtw = EPI == QIM_EPI_QK_NORM_ROPE && p.vt && col0 >= p.qk_cols;
     float bias[TJ] = {};
     if constexpr (EPI == QIM_EPI_BIAS) {
 #pragma unroll
@@ -382,6 +394,12 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
                         *reinterpret_cast<uint2 *>(grp + epi_col_offset<W>(u * 32 + lr)) =
                             make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
                     }
+                } else if (vtw) {
+#pragma unroll
+                    for (int tj = 0; tj < TJ; ++tj)
+                        *reinterpret_cast<uint2 *>(reg + (tj * 32 + lr) * VT_COL + (32 * tl + 8 * ig + 4 * kh) * 2) =
+                            make_uint2(pack_bf16x2(acc[ti][tj][4 * ig + 0], acc[ti][tj][4 * ig + 1]),
+                                       pack_bf16x2(acc[ti][tj][4 * ig + 2], acc[ti][tj][4 * ig + 3]));
                 } else {
 #pragma unroll
                     for (int tj = 0; tj < TJ; ++tj) {
@@ -398,6 +416,27 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
             }
         }
         // pass 2 (LDS operations of one wave complete in order: no wait needed)
+        if (vtw) {
+            // V^T tiles: this half's 64 rows are one key block (seq % 64 ==
+            // 0).  Tile row d is 8 chunks of 16 bytes; physical chunk pc holds
+            // logical chunk c = pc ^ ((d >> 1) & 7): keys 16(c/2) + 4(c%2) +
+            // 0..3, then the same 8 keys later.  Eight lanes per row: each
+            // store instruction writes 1 KiB contiguous.
+            const int64_t R = row0 + half * 64;
+            if (R < p.M) {
+                const int64_t bt = R / p.seq, kb = (R - bt * p.seq) / 64, vc = col0 - p.qk_cols;
+                uint16_t *tile = p.vt + ((bt * (p.q_cols / 128) + vc / 128) * p.vt_nkb + kb) * (64 * 128);
+#pragma unroll
+                for (int it = 0; it < W / 8; ++it) {
+                    const int dl = it * 8 + (lane >> 3), pc = lane & 7, d = (int)(vc & 127) + dl;
+                    const int c = pc ^ ((d >> 1) & 7), k0 = 16 * (c >> 1) + 4 * (c & 1);
+                    const uint2 lo = *reinterpret_cast<const uint2 *>(reg + dl * VT_COL + k0 * 2);
+                    const uint2 hi = *reinterpret_cast<const uint2 *>(reg + dl * VT_COL + (k0 + 8) * 2);
+                    st_nt(tile + d * 64 + pc * 8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+                }
+            }
+            continue;
+        }
         const int cl = lane % LPR, gl = lane / LPR;
 #pragma unroll
         for (int it = 0; it < 16 / GPI; ++it) {
@@ -711,6 +750,7 @@ struct QKNormRope {
     const void *wq, *wk, *freqs;
     float epsq, epsk;
     int64_t heads;
+    void *vt;  // V^T tiles instead of the V columns of out, or null
 };
 
 static int gemm_run(const void *aq, const void *as, const void *bq, const void *bs, int64_t M, int64_t N, int64_t K,
@@ -739,7 +779,7 @@ static int gemm_run(const void *aq, const void *as, const void *bq, const void *
                (uint8_t *)out_scales, (int)tiles_m, (int)tiles_n, 0,
                (layouts & QIM_GEMM_A_TILED) != 0, (layouts & QIM_GEMM_B_TILED) != 0,
                (layouts & QIM_GEMM_OUT_TILED) != 0,
-               nullptr, nullptr, nullptr, 0.0f, 0.0f, 0, 0};
+               nullptr, nullptr, nullptr, 0.0f, 0.0f, 0, 0, nullptr, 0};
     if (qk) {
         a.wq = (const uint16_t *)qk->wq;
         a.wk = (const uint16_t *)qk->wk;
@@ -748,6 +788,8 @@ static int gemm_run(const void *aq, const void *as, const void *bq, const void *
         a.epsk = qk->epsk;
         a.q_cols = qk->heads * 128;
         a.qk_cols = 2 * qk->heads * 128;
+        a.vt = static_cast<uint16_t *>(qk->vt);
+        a.vt_nkb = seq / 64;
     }
     const int64_t tiles = tiles_m * tiles_n;
     a.main_tiles = (int)main_tile_count(tiles);
@@ -803,20 +845,38 @@ extern "C" int qim_mxfp8_gemm_ex(const void *aq, const void *as, const void *bq,
                     stream);
 }
 
+static int qk_norm_rope_run(const char *who, const void *aq, const void *as, const void *bq, const void *bs, int64_t M,
+                            int64_t K, int64_t H, int layouts, const void *wq, const void *wk, const void *freqs,
+                            int64_t seq, float epsq, float epsk, void *out, int64_t ldo, void *vt, void *stream) {
+    QIM_REQUIRE(wq && wk && freqs, QIM_ERR_ARG, "%s: null pointer", who);
+    QIM_REQUIRE(H > 0 && H % 2 == 0 && H < (1 << 20), QIM_ERR_SHAPE,
+                "%s: H=%lld must be even (N = 3 H 128 %% 256 == 0)", who, (long long)H);
+    QIM_REQUIRE(seq > 0 && seq < (1ll << 31) && M < (1ll << 31), QIM_ERR_SHAPE, "%s: seq=%lld / M=%lld out of range",
+                who, (long long)seq, (long long)M);
+    QIM_REQUIRE(aligned16(wq) && aligned16(wk) && aligned16(freqs) && aligned16(vt), QIM_ERR_LAYOUT,
+                "%s: wq, wk, freqs (and vt) must be 16-byte aligned", who);
+    QIM_REQUIRE((layouts & QIM_GEMM_OUT_TILED) == 0, QIM_ERR_ARG, "%s: the output is bf16 (no tiled output)", who);
+    const QKNormRope qk{wq, wk, freqs, epsq, epsk, H, vt};
+    return gemm_run(aq, as, bq, bs, M, 3 * H * 128, K, QIM_EPI_QK_NORM_ROPE, layouts, nullptr, nullptr, nullptr, seq,
+                    out, ldo, nullptr, &qk, stream);
+}
+
 extern "C" int qim_mxfp8_gemm_qk_norm_rope(const void *aq, const void *as, const void *bq, const void *bs,
                                            int64_t M, int64_t K, int64_t H, int layouts, const void *wq,
                                            const void *wk, const void *freqs, int64_t seq, float epsq, float epsk,
                                            void *out, int64_t ldo, void *stream) {
-    QIM_REQUIRE(wq && wk && freqs, QIM_ERR_ARG, "qim_mxfp8_gemm_qk_norm_rope: null pointer");
-    QIM_REQUIRE(H > 0 && H % 2 == 0 && H < (1 << 20), QIM_ERR_SHAPE,
-                "qim_mxfp8_gemm_qk_norm_rope: H=%lld must be even (N = 3 H 128 %% 256 == 0)", (long long)H);
-    QIM_REQUIRE(seq > 0 && seq < (1ll << 31) && M < (1ll << 31), QIM_ERR_SHAPE,
-                "qim_mxfp8_gemm_qk_norm_rope: seq=%lld / M=%lld out of range", (long long)seq, (long long)M);
-    QIM_REQUIRE(aligned16(wq) && aligned16(wk) && aligned16(freqs), QIM_ERR_LAYOUT,
-                "qim_mxfp8_gemm_qk_norm_rope: wq, wk, freqs must be 16-byte aligned");
-    QIM_REQUIRE((layouts & QIM_GEMM_OUT_TILED) == 0, QIM_ERR_ARG,
-                "qim_mxfp8_gemm_qk_norm_rope: the output is bf16 (no tiled output)");
-    const QKNormRope qk{wq, wk, freqs, epsq, epsk, H};
-    return gemm_run(aq, as, bq, bs, M, 3 * H * 128, K, QIM_EPI_QK_NORM_ROPE, layouts, nullptr, nullptr, nullptr, seq,
-                    out, ldo, nullptr, &qk, stream);
+    return qk_norm_rope_run("qim_mxfp8_gemm_qk_norm_rope", aq, as, bq, bs, M, K, H, layouts, wq, wk, freqs, seq, epsq,
+                            epsk, out, ldo, nullptr, stream);
+}
+
+extern "C" int qim_mxfp8_gemm_qk_norm_rope_vt(const void *aq, const void *as, const void *bq, const void *bs,
+                                              int64_t M, int64_t K, int64_t H, int layouts, const void *wq,
+                                              const void *wk, const void *freqs, int64_t seq, float epsq,
+                                              float epsk, void *out, int64_t ldo, void *vt, void *stream) {
+    QIM_REQUIRE(vt, QIM_ERR_ARG, "qim_mxfp8_gemm_qk_norm_rope_vt: null vt");
+    QIM_REQUIRE(seq > 0 && seq % 64 == 0 && M % seq == 0, QIM_ERR_SHAPE,
+                "qim_mxfp8_gemm_qk_norm_rope_vt: seq=%lld must be a multiple of 64 dividing M=%lld", (long long)seq,
+                (long long)M);
+    return qk_norm_rope_run("qim_mxfp8_gemm_qk_norm_rope_vt", aq, as, bq, bs, M, K, H, layouts, wq, wk, freqs, seq,
+                            epsq, epsk, out, ldo, vt, stream);
 }

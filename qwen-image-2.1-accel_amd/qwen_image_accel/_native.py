@@ -59,6 +59,8 @@ SIGNATURES = {
     "qim_mxfp8_gemm": (_C, [_P, _P, _P, _P, _I, _I, _I, _C, _P, _P, _P, _I, _P, _I, _P, _P]),
     "qim_mxfp8_gemm_ex": (_C, [_P, _P, _P, _P, _I, _I, _I, _C, _C, _P, _P, _P, _I, _P, _I, _P, _P]),
     "qim_mxfp8_gemm_qk_norm_rope": (_C, [_P, _P, _P, _P, _I, _I, _I, _C, _P, _P, _P, _I, _F, _F, _P, _I, _P]),
+    "qim_mxfp8_gemm_qk_norm_rope_vt": (_C, [_P, _P, _P, _P, _I, _I, _I, _C, _P, _P, _P, _I, _F, _F, _P, _I, _P,
+                                           _P]),
     "qim_attention": (_C, [_P, _I, _P, _I, _P, _I, _P, _I, _P, _I, _I, _I, _I, _I, _I, _F, _P]),
     "qim_attention_workspace_bytes": (_I, [_I, _I, _I, _I, _I]),
     "qim_attention_mxfp8": (_C, [_P, _I, _P, _I, _P, _I, _P, _P, _C, _P, _I, _I, _I, _I, _I, _I, _F, _P]),

@@ -11,7 +11,9 @@ modulation, fused QKV projection, hidden 3072, 24 heads x 128, FFN 12288):
                                                             qim_mxfp8_gemm_qk_norm_rope
     o   = attention(q, k, v)        -- qim_attention (attention_fn); stand-in o = v
     h   = h + tanh(g1) * (MXFP8(o) @ W_out)                 qim_mx_quantize + GEMM epilogue
-          (MXFP8(attention(q, k, v)) in one pass:           qim_attention_mxfp8)
+          (fused_attention: V leaves the QKV GEMM as the attention's V^T
+          tiles, qim_mxfp8_gemm_qk_norm_rope_vt, and MXFP8(attention(q, k,
+          v)) is one pass, qim_attention_mxfp8)
     x   = MXFP8(LN(h) * (1 + scale2) + shift2)             qim_adaln_quantize
     a   = MXFP8(silu(x @ W_gate) * (x @ W_up))              GEMM, SwiGLU->MXFP8 epilogue
     h   = h + tanh(g2) * (a @ W_down)                       GEMM, gated-residual epilogue
@@ -29,7 +31,7 @@ from dataclasses import dataclass
 
 import torch
 
-from qwen_image_accel.kernels import gemm, mxfp8
+from qwen_image_accel.kernels import attention, gemm, mxfp8
 from qwen_image_accel.kernels.epilogue import layer_norm_scale_quantize
 
 
@@ -82,14 +84,19 @@ class MMDiTBlock:
         return MMDiTBlock.from_weights(w(3 * dim, dim), w(dim, dim), w(ffn, dim), w(ffn, dim),
                                        w(dim, ffn), nq, nk, heads)
 
-    def forward(self, h, modulation, freqs, attention_fn=None, attention_mxfp8_fn=None):
+    def forward(self, h, modulation, freqs, attention_fn=None, attention_mxfp8_fn=None, fused_attention=False):
         """h: (B, S, dim) bf16; modulation: (B, 6, dim) bf16 rows
         (shift1, scale1, gate1, shift2, scale2, gate2); freqs: (S, head_dim/2)
         complex64.  ``attention_fn(q, k, v) -> (B, S, dim)`` defaults to the
         stand-in that returns v.  ``attention_mxfp8_fn(q, k, v)`` (e.g.
         ``attention.attention_mxfp8``), when given, returns the attention
         output already quantized in the tiled layout (the same bytes as
-        quantizing attention_fn's output) and replaces both."""
+        quantizing attention_fn's output) and replaces both.
+        ``fused_attention=True`` runs the library's attention core with both
+        of its fusions: the QKV projection writes V straight into the
+        attention's V^T tiles (S % 64 == 0) and the attention writes the
+        out-projection's MXFP8 input -- the same bytes as
+        ``attention_fn=attention.attention``."""
         b, s, d = h.shape
         shift1, scale1, g1, shift2, scale2, g2 = (modulation[:, i:i + 1] for i in range(6))
         gate1, gate2 = g1.tanh(), g2.tanh()
@@ -98,13 +105,20 @@ class MMDiTBlock:
 
         x = layer_norm_scale_quantize(h, scale1.contiguous(), norm, shift=shift1.contiguous(),
                                       add_one=True, tiled=True)
+        ws = None
+        if fused_attention:
+            if s % 64:
+                raise ValueError(f"fused_attention needs S % 64 == 0 (S = {s})")
+            ws = attention.workspace(b, s, s, self.heads, h.device)
         qkv = gemm.mx_matmul_qk_norm_rope(x, self.w_qkv.values, self.w_qkv.scales, self.norm_q, self.norm_k,
-                                          freqs, self.heads, s, self.eps, self.eps, weight_tiled=True)
+                                          freqs, self.heads, s, self.eps, self.eps, weight_tiled=True, vt=ws)
         qkv4 = qkv.view(b, s, 3 * d)
         q = qkv4[:, :, :d].unflatten(-1, (self.heads, hd))                      # normalised + rotated
         k = qkv4[:, :, d:2 * d].unflatten(-1, (self.heads, hd))
         v = qkv4[:, :, 2 * d:].unflatten(-1, (self.heads, hd))
-        if attention_mxfp8_fn is not None:
+        if fused_attention:
+            oq = attention.attention_mxfp8(q, k, None, workspace=ws)   # V^T already in ws
+        elif attention_mxfp8_fn is not None:
             oq = attention_mxfp8_fn(q, k, v)
         else:
             o = qkv[:, 2 * d:] if attention_fn is None else attention_fn(q, k, v).reshape(b * s, d)  # stand-in: v

@@ -49,57 +49,66 @@ def prepare_attention_inputs(q, k, v, norm_q, norm_k, freqs, cached_k, cached_v)
     return oq, ok, ov
 
 
-def attention(q, k, v, scale=None, out=None):
+def workspace(b, s, t, h, device, d=128):
+    """A workspace for ``attention`` / ``attention_mxfp8`` of this shape (V^T
+    tiles first, then the split items' partial results)."""
+    with torch.cuda.device(device):
+        nbytes = _native.lib().qim_attention_workspace_bytes(b, s, t, h, d)
+    if nbytes <= 0:
+        raise _native.Unsupported("attention", _native.QIM_ERR_SHAPE, f"head dim {d} (128 only)")
+    return torch.empty(nbytes, device=device, dtype=torch.uint8)
+
+
+def _common(name, q, k, v, ws):
+    b, s, h, d = q.shape
+    t = k.shape[1]
+    for x, n in ((q, s), (k, t), (v, t)):
+        if x is None:
+            continue
+        if (x.dtype != torch.bfloat16 or not x.is_cuda or x.shape != (b, n, h, d) or x.stride(3) != 1
+                or x.stride(2) != d or x.stride(0) != n * x.stride(1)):
+            raise _native.Unsupported(name, _native.QIM_ERR_LAYOUT,
+                                      "expects bf16 (B, N, H, D) tensors with packed heads and token rows")
+    if v is None and ws is None:
+        raise ValueError(f"{name}: v=None needs the workspace holding V^T")
+    if ws is None:
+        ws = workspace(b, s, t, h, q.device, d)
+    vp, ldv = (None, 0) if v is None else (_native.ptr(v), v.stride(1))
+    return b, s, t, h, d, vp, ldv, ws
+
+
+def attention(q, k, v, scale=None, out=None, *, workspace=None):
     """softmax(q k^T * scale) v per (batch, head): libqim's ``qim_attention``.
 
     q: (B, S, H, 128), k, v: (B, T, H, 128) bf16 on the GPU, each with unit
     stride inside a token and any token stride (e.g. views into a fused QKV
     projection).  scale defaults to 1/sqrt(128).  Returns (B, S, H, 128) bf16.
+    ``workspace``: from ``attention.workspace`` (allocated per call if None);
+    with ``v=None`` it must already hold V^T, written by the QKV projection
+    (``gemm.mx_matmul_qk_norm_rope(..., vt=workspace)``, T % 64 == 0).
     The block's attention core; the reference calls torch SDPA there
     (optimizations/quantized_decode.py:70-77)."""
-    b, s, h, d = q.shape
-    t = k.shape[1]
-    for x, n in ((q, s), (k, t), (v, t)):
-        if (x.dtype != torch.bfloat16 or not x.is_cuda or x.shape != (b, n, h, d) or x.stride(3) != 1
-                or x.stride(2) != d or x.stride(0) != n * x.stride(1)):
-            raise _native.Unsupported("attention", _native.QIM_ERR_LAYOUT,
-                                      "expects bf16 (B, N, H, D) tensors with packed heads and token rows")
+    b, s, t, h, d, vp, ldv, ws = _common("attention", q, k, v, workspace)
     if out is None:
         out = torch.empty((b, s, h, d), device=q.device, dtype=torch.bfloat16)
-    with torch.cuda.device(q.device):
-        nbytes = _native.lib().qim_attention_workspace_bytes(b, s, t, h, d)
-    if nbytes <= 0:
-        raise _native.Unsupported("attention", _native.QIM_ERR_SHAPE, f"head dim {d} (128 only)")
-    ws = torch.empty(nbytes, device=q.device, dtype=torch.uint8)
-    _native.call("qim_attention", _native.ptr(q), q.stride(1), _native.ptr(k), k.stride(1), _native.ptr(v),
-                 v.stride(1), _native.ptr(out), out.stride(1), _native.ptr(ws), nbytes, b, s, t, h, d,
+    _native.call("qim_attention", _native.ptr(q), q.stride(1), _native.ptr(k), k.stride(1), vp, ldv,
+                 _native.ptr(out), out.stride(1), _native.ptr(ws), ws.numel(), b, s, t, h, d,
                  float(scale if scale is not None else d ** -0.5), _native.stream(q.device))
     return out
 
 
-def attention_mxfp8(q, k, v, scale=None, *, tiled=True, out=None):
+def attention_mxfp8(q, k, v, scale=None, *, tiled=True, out=None, workspace=None):
     """``mxfp8.quantize(attention(q, k, v).reshape(B*S, H*128), tiled=tiled)``
     in one pass (libqim's ``qim_attention_mxfp8``): the same codes and scales,
     without the bf16 output.  The block's out-projection input; the reference
     runs SDPA and then its quantize kernel (optimizations/quantized_decode.py:
     70-96).  ``out``: a preallocated ``mxfp8.empty_quantized(B*S, H*128,
-    device, tiled=tiled)``."""
-    b, s, h, d = q.shape
-    t = k.shape[1]
-    for x, n in ((q, s), (k, t), (v, t)):
-        if (x.dtype != torch.bfloat16 or not x.is_cuda or x.shape != (b, n, h, d) or x.stride(3) != 1
-                or x.stride(2) != d or x.stride(0) != n * x.stride(1)):
-            raise _native.Unsupported("attention_mxfp8", _native.QIM_ERR_LAYOUT,
-                                      "expects bf16 (B, N, H, D) tensors with packed heads and token rows")
-    with torch.cuda.device(q.device):
-        nbytes = _native.lib().qim_attention_workspace_bytes(b, s, t, h, d)
-    if nbytes <= 0:
-        raise _native.Unsupported("attention_mxfp8", _native.QIM_ERR_SHAPE, f"head dim {d} (128 only)")
+    device, tiled=tiled)``; ``workspace`` and ``v=None`` as for ``attention``."""
+    b, s, t, h, d, vp, ldv, ws = _common("attention_mxfp8", q, k, v, workspace)
     if out is None:
         out = mxfp8.empty_quantized(b * s, h * d, q.device, tiled=tiled)
-    ws = torch.empty(nbytes, device=q.device, dtype=torch.uint8)
-    _native.call("qim_attention_mxfp8", _native.ptr(q), q.stride(1), _native.ptr(k), k.stride(1), _native.ptr(v),
-                 v.stride(1), _native.ptr(out.values), _native.ptr(out.scales), int(tiled), _native.ptr(ws), nbytes,
+    _native.call("qim_attention_mxfp8", _native.ptr(q), q.stride(1), _native.ptr(k), k.stride(1), vp, ldv,
+                 _native.ptr(out.values), _native.ptr(out.scales), int(tiled), _native.ptr(ws), ws.numel(),
                  b, s, t, h, d, float(scale if scale is not None else d ** -0.5), _native.stream(q.device))
     return out
 

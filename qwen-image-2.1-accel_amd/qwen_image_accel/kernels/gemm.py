@@ -22,7 +22,7 @@ EPILOGUES = {
 
 
 def mx_matmul_qk_norm_rope(activation, weight_fp8, weight_scale, weight_q, weight_k, freqs, heads, seq,
-                           eps_q=1e-6, eps_k=1e-6, *, weight_tiled=False, out=None):
+                           eps_q=1e-6, eps_k=1e-6, *, weight_tiled=False, out=None, vt=None):
     """The MMDiT block's QKV projection with QK-RMSNorm + RoPE in its epilogue.
 
     Returns the bf16 ``(rows, 3 * heads * 128)`` projection whose Q and K
@@ -30,7 +30,13 @@ def mx_matmul_qk_norm_rope(activation, weight_fp8, weight_scale, weight_q, weigh
     ``kernels.attention.qk_norm_rope`` computes on the unfused output -- and
     whose V columns are the plain product.  ``freqs``: complex64 (seq, 64),
     row = output row % seq.  No reference counterpart as one call: it fuses
-    kernels/attention.py:16-89 into optimizations/mxfp8.py:32-36."""
+    kernels/attention.py:16-89 into optimizations/mxfp8.py:32-36.
+
+    ``vt``: an attention workspace (``attention.workspace``; seq % 64 == 0,
+    rows a multiple of seq): the V columns are written there as the
+    attention core's V^T tiles instead of into the output, whose V columns
+    are then left unwritten; pass ``v=None`` and this workspace to
+    ``attention.attention`` / ``attention_mxfp8``."""
     a = activation
     w = weight_fp8 if weight_tiled else weight_rows(weight_fp8)
     n, k = w.shape
@@ -45,10 +51,15 @@ def mx_matmul_qk_norm_rope(activation, weight_fp8, weight_scale, weight_q, weigh
         raise ValueError("out must be a bf16 (rows, N) tensor with unit column stride")
     layouts = (_native.GEMM_A_TILED if a.tiled else 0) | (_native.GEMM_B_TILED if weight_tiled else 0)
     f = torch.view_as_real(freqs.contiguous())
-    _native.call("qim_mxfp8_gemm_qk_norm_rope", _native.ptr(a.values), _native.ptr(a.scales), _native.ptr(w),
-                 _native.ptr(weight_scale), m, k, heads, layouts, _native.ptr(weight_q), _native.ptr(weight_k),
-                 _native.ptr(f), seq, float(eps_q), float(eps_k), _native.ptr(out), out.stride(0),
-                 _native.stream(out.device))
+    args = (_native.ptr(a.values), _native.ptr(a.scales), _native.ptr(w), _native.ptr(weight_scale), m, k, heads,
+            layouts, _native.ptr(weight_q), _native.ptr(weight_k), _native.ptr(f), seq, float(eps_q), float(eps_k),
+            _native.ptr(out), out.stride(0))
+    if vt is None:
+        _native.call("qim_mxfp8_gemm_qk_norm_rope", *args, _native.stream(out.device))
+    else:
+        if vt.numel() * vt.element_size() < m // seq * heads * seq * 256:
+            raise ValueError("vt workspace too small")
+        _native.call("qim_mxfp8_gemm_qk_norm_rope_vt", *args, _native.ptr(vt), _native.stream(out.device))
     return out
 
 

@@ -59,3 +59,35 @@ def test_qkv_gemm_rejects_odd_heads(dev):
     freqs = torch.ones(128, 64, dtype=torch.complex64, device=dev)
     with pytest.raises(_native.Unsupported):
         gemm.mx_matmul_qk_norm_rope(aq, w8.values, w8.scales, wq, wq, freqs, 3, 128)
+
+
+# 4352 x 24 heads: 612 tiles, whole tiles then quarter tiles (two waves per
+# head); 2 x 320 rows: quarter tiles only, two batches.
+@pytest.mark.parametrize("m,heads,k,seq", [(4352, 24, 256, 4352), (640, 4, 256, 320)])
+def test_qkv_gemm_writes_attention_vt(dev, m, heads, k, seq):
+    """qim_mxfp8_gemm_qk_norm_rope_vt: the V columns leave as the attention's
+    V^T tiles.  Attention from those tiles (v = None) equals attention on the
+    plain projection's V, bit for bit, and the Q/K columns are unchanged."""
+    say("qkv vt", m, heads, k, seq)
+    g = torch.Generator().manual_seed(m + heads)
+    d = heads * 128
+    a = bf16_randn(g, (m, k)).to(dev)
+    w = bf16_randn(g, (3 * d, k), 0.05).to(dev)
+    wq = (torch.rand(128, generator=g) * 0.4 + 0.8).to(torch.bfloat16).to(dev)
+    wk = (torch.rand(128, generator=g) * 0.4 + 0.8).to(torch.bfloat16).to(dev)
+    ang = torch.rand(seq, 64, generator=g, dtype=torch.float64) * 6.283185307179586
+    freqs = torch.polar(torch.ones_like(ang), ang).to(torch.complex64).to(dev)
+    b = m // seq
+    aq = mxfp8.quantize(a, tiled=True)
+    w8 = mxfp8.quantize(w, tiled=True)
+    plain = gemm.mx_matmul_qk_norm_rope(aq, w8.values, w8.scales, wq, wk, freqs, heads, seq, weight_tiled=True)
+    ws = attention.workspace(b, seq, seq, heads, dev)
+    ws.fill_(0xff)
+    fused = gemm.mx_matmul_qk_norm_rope(aq, w8.values, w8.scales, wq, wk, freqs, heads, seq, weight_tiled=True,
+                                        vt=ws)
+    assert torch.equal(fused[:, :2 * d], plain[:, :2 * d])
+    q, k_, v = (plain.view(b, seq, 3 * d)[:, :, i * d:(i + 1) * d].unflatten(-1, (heads, 128)) for i in range(3))
+    ref = attention.attention(q, k_, v)
+    got = attention.attention(q, k_, None, workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)

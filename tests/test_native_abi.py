@@ -74,6 +74,14 @@ def test_abi_version():
      _native.QIM_ERR_ARG),
     ("qim_attention", (18, 3072, 16, 3072, 16, 3072, 16, 3072, 16, 1 << 40, 1, 256, 256, 24, 128, 0.1, None),
      _native.QIM_ERR_LAYOUT),
+    # QKV GEMM writing V^T: null vt; seq not a multiple of 64
+    ("qim_mxfp8_gemm_qk_norm_rope_vt", (16, 16, 16, 16, 4352, 256, 24, 0, 16, 16, 16, 4352, 1e-6, 1e-6, 16, 9216,
+                                        None, None), _native.QIM_ERR_ARG),
+    ("qim_mxfp8_gemm_qk_norm_rope_vt", (16, 16, 16, 16, 4350, 256, 24, 0, 16, 16, 16, 4350, 1e-6, 1e-6, 16, 9216,
+                                        16, None), _native.QIM_ERR_SHAPE),
+    # attention with V^T from the workspace (v null) needs T % 64 == 0
+    ("qim_attention", (16, 3072, 16, 3072, None, 0, 16, 3072, 16, 1 << 40, 1, 256, 250, 24, 128, 0.1, None),
+     _native.QIM_ERR_SHAPE),
     # attention_mxfp8: null scales; tiled 2; misaligned codes
     ("qim_attention_mxfp8", (16, 3072, 16, 3072, 16, 3072, 16, None, 1, 16, 1 << 40, 1, 256, 256, 24, 128, 0.1,
                              None), _native.QIM_ERR_ARG),
