@@ -331,7 +331,7 @@ __device__ __forceinline__ float silu_exact(float g) { return g / (1.0f + expf(-
 // silu_exact for every bf16 input with |g| < 64 (measured exhaustively).
 constexpr uint32_t SILU_BAND = 8;
 
-// bf16(silu(g)) for a bf16 value g, bit-identical to rbf(silu_exact(g)).
+// bf16(silu(g)) for bf16 values g, bit-identical to rbf(silu_exact(g)).
 // Fast path: e^-g = 2^t (v_exp_f32) with the rounding error of t = -g log2(e)
 // folded back in to first order, and a hardware reciprocal (v_rcp_f32); its
 // result is used when it lies more than SILU_BAND ulps from a bf16 rounding
@@ -339,7 +339,7 @@ constexpr uint32_t SILU_BAND = 8;
 // rare rest (about 2^-12 of the inputs) and |g| >= 64 (where v_rcp_f32 flushes
 // the tiny reciprocal of 1 + e^-g) take the exact path.  An exhaustive GPU test
 // over all 65536 bf16 inputs checks the identity.
-__device__ __forceinline__ float silu_bf16(float g) {
+__device__ __forceinline__ float silu_fast(float g) {
     constexpr float NL1 = -1.44269502f;                    // -log2(e), rounded
     constexpr float NL2 = -1.92596299e-08f;                // -(log2(e) - 1.44269502f)
     const float t = g * NL1;
@@ -347,11 +347,46 @@ __device__ __forceinline__ float silu_bf16(float g) {
     r = __builtin_fmaf(g, NL2, r);
     float e = __builtin_amdgcn_exp2f(t);
     e = __builtin_fmaf(e * r, 0.693147181f, e);            // e * 2^r to first order
-    const float y = g * __builtin_amdgcn_rcpf(1.0f + e);
-    const uint32_t u = __float_as_uint(y);
-    const bool near = ((u + (SILU_BAND - 0x8000u)) & 0xffffu) < 2u * SILU_BAND;
-    if (__builtin_expect(near || !(__builtin_fabsf(g) < 64.0f), 0)) return rbf(silu_exact(g));
-    return rbf(y);
+    return g * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+// Distance (mod 2^16, in fp32 ulps, offset by SILU_BAND) of y from the next
+// bf16 rounding midpoint: below 2 * SILU_BAND means "within the band".
+__device__ __forceinline__ uint32_t silu_band_key(float y) {
+    return (__float_as_uint(y) + (SILU_BAND - 0x8000u)) & 0xffffu;
+}
+
+// N values at once: the N fast estimates (independent chains the scheduler
+// can interleave), rounded in pairs; the band test and the |g| < 64 test are
+// folded into a running minimum and maximum, and one rarely taken branch
+// redoes, exactly, the values that need it.  y[i] is rounded to bf16.
+template <int N>
+__device__ __forceinline__ void silu_bf16_n(const float *g, float *y) {
+    uint32_t key = 0xffffu;
+    float gmax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        y[i] = silu_fast(g[i]);
+        const uint32_t k = silu_band_key(y[i]);
+        key = k < key ? k : key;
+        gmax = __builtin_fmaxf(gmax, __builtin_fabsf(g[i]));  // NaN inputs: y is NaN either way
+    }
+#pragma unroll
+    for (int i = 0; i + 1 < N; i += 2) rbf2(y[i], y[i + 1]);
+    if constexpr (N % 2) y[N - 1] = rbf(y[N - 1]);
+    if (__builtin_expect(key < 2u * SILU_BAND || !(gmax < 64.0f), 0)) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            const float f = silu_fast(g[i]);
+            if (silu_band_key(f) < 2u * SILU_BAND || !(__builtin_fabsf(g[i]) < 64.0f)) y[i] = rbf(silu_exact(g[i]));
+        }
+    }
+}
+
+__device__ __forceinline__ float silu_bf16(float g) {
+    float y;
+    silu_bf16_n<1>(&g, &y);
+    return y;
 }
 
 // swiglu element: bf16(bf16(silu(g)) * v) with an fp32 multiply.

@@ -43,8 +43,9 @@ __global__ __launch_bounds__(256) void k_swiglu(const uint16_t *__restrict__ g, 
     float gf[8], vf[8], o[8];
     unpack8(gv, gf);
     unpack8(vv, vf);
+    silu_bf16_n<8>(gf, o);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = silu_bf16(gf[i]) * vf[i];
+    for (int i = 0; i < 8; ++i) o[i] *= vf[i];
     st_nt(out + row * ldo + c * 8, pack8(o));
 }
 

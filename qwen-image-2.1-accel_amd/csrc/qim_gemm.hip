@@ -385,15 +385,27 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
             for (int ig = 0; ig < 4; ++ig) {
                 uint8_t *grp = reg + (tl * 8 + ig * 2 + kh) * RGS;  // rows 32tl + 8ig + 4kh + 0..3
                 if constexpr (SWI) {
+                    // swiglu1 on TJ / 2 x 4 values with one exact-path branch;
+                    // the store's bf16 packing is the final rounding.
+                    constexpr int NS = TJ / 2 * 4;
+                    float gs[NS], us[NS], y[NS];
 #pragma unroll
-                    for (int u = 0; u < TJ / 2; ++u) {
-                        float y[4];
+                    for (int u = 0; u < TJ / 2; ++u)
 #pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            y[e] = swiglu1(rbf(acc[ti][2 * u][4 * ig + e]), rbf(acc[ti][2 * u + 1][4 * ig + e]));
+                        for (int e = 0; e < 4; e += 2) {
+                            gs[4 * u + e] = acc[ti][2 * u][4 * ig + e];
+                            gs[4 * u + e + 1] = acc[ti][2 * u][4 * ig + e + 1];
+                            us[4 * u + e] = acc[ti][2 * u + 1][4 * ig + e];
+                            us[4 * u + e + 1] = acc[ti][2 * u + 1][4 * ig + e + 1];
+                            rbf2(gs[4 * u + e], gs[4 * u + e + 1]);
+                            rbf2(us[4 * u + e], us[4 * u + e + 1]);
+                        }
+                    silu_bf16_n<NS>(gs, y);
+#pragma unroll
+                    for (int u = 0; u < TJ / 2; ++u)
                         *reinterpret_cast<uint2 *>(grp + epi_col_offset<W>(u * 32 + lr)) =
-                            make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
-                    }
+                            make_uint2(pack_bf16x2(y[4 * u] * us[4 * u], y[4 * u + 1] * us[4 * u + 1]),
+                                       pack_bf16x2(y[4 * u + 2] * us[4 * u + 2], y[4 * u + 3] * us[4 * u + 3]));
                 } else if (vtw) {
 #pragma unroll
                     for (int tj = 0; tj < TJ; ++tj)

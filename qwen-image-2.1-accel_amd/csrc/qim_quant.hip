@@ -42,11 +42,12 @@ struct SwigluSource {
         b = live ? ld_nt(v + row * ldv + col) : make_uint4(0, 0, 0, 0);
     }
     __device__ __forceinline__ void values(const uint4 &a, const uint4 &b, float *f) const {
-        float gg[8], vv[8];
+        float gg[8], vv[8], s[8];
         unpack8(a, gg);
         unpack8(b, vv);
+        silu_bf16_n<8>(gg, s);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) f[i] = swiglu1(gg[i], vv[i]);
+        for (int i = 0; i < 8; ++i) f[i] = rbf(s[i] * vv[i]);
     }
 };
 

@@ -133,9 +133,23 @@ __global__ void k_debug_mfma_probe(float *__restrict__ out) {
     }
 }
 
+// bf16(silu(g)): odd threads through silu_bf16, even ones through the batched
+// silu_bf16_n<8> on g[i .. i+7] (one element kept), so an exhaustive sweep
+// covers both forms.
 __global__ void k_debug_silu(const uint16_t *__restrict__ g, uint16_t *__restrict__ out, int64_t n) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) out[i] = (uint16_t)(__float_as_uint(silu_bf16(bf16_to_f32(g[i]))) >> 16);
+    if (i >= n) return;
+    float y;
+    if (i & 1) {
+        y = silu_bf16(bf16_to_f32(g[i]));
+    } else {
+        float x[8], r[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = bf16_to_f32(g[i + j < n ? i + j : i]);
+        silu_bf16_n<8>(x, r);
+        y = r[0];
+    }
+    out[i] = (uint16_t)(__float_as_uint(y) >> 16);
 }
 
 // Streaming copy, one 16-byte vector per lane: the achievable-bandwidth
