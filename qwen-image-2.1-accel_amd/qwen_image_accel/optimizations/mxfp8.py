@@ -17,7 +17,7 @@ import torch
 from torch import nn
 
 from qwen_image_accel.kernels.gemm import mx_matmul
-from qwen_image_accel.kernels.mxfp8 import Quantized, quantize, tile_codes, untile_codes
+from qwen_image_accel.kernels.mxfp8 import Quantized, padded_rows, quantize, tile_codes, untile_codes
 
 
 def _supported(k, n):
@@ -41,6 +41,24 @@ class MXFP8Linear(nn.Module):
         self.register_buffer("weight_scale", quantized.scales)
         self.register_buffer("bias", None if linear.bias is None
                              else linear.bias.detach().to(torch.bfloat16).contiguous())
+
+    @classmethod
+    def from_quantized(cls, in_features, out_features, weight_tiled, weight_scale, bias=None):
+        """An ``MXFP8Linear`` holding already quantized bytes, without quantizing:
+        the (N, K) E4M3 codes in the tiled layout (N padded to 128) and the
+        swizzled E8M0 scales, as ``weight_tiled`` / ``weight_scale`` hold them."""
+        rows = padded_rows(out_features)
+        codes = weight_tiled.view(torch.float8_e4m3fn)
+        scales = weight_scale.view(torch.float8_e8m0fnu).reshape(-1)
+        if codes.shape != (rows, in_features) or scales.numel() != rows * in_features // 32:
+            raise ValueError(f"quantized weight does not match a ({out_features}, {in_features}) linear")
+        self = cls.__new__(cls)
+        nn.Module.__init__(self)
+        self.in_features, self.out_features = in_features, out_features
+        self.register_buffer("weight_tiled", codes)
+        self.register_buffer("weight_scale", scales)
+        self.register_buffer("bias", bias)
+        return self
 
     def matmul(self, activation, dtype=torch.bfloat16, **epilogue):
         """Multiply an already quantized activation; several weights can share one.

@@ -12,11 +12,13 @@ import types
 
 from qwen_image_accel.kernels.bf16 import swiglu
 from qwen_image_accel.kernels.elementwise import residual
+from qwen_image_accel.kernels.gemm import mx_matmul
 from qwen_image_accel.kernels.epilogue import layer_norm_scale_quantize, swiglu_quantize
 from qwen_image_accel.kernels.layernorm import layer_norm_scale
 from qwen_image_accel.kernels.mxfp8 import Quantized, quantize
 from qwen_image_accel.optimizations.fusion import _attend, modulation_values
 from qwen_image_accel.optimizations.mxfp8 import MXFP8Linear
+from qwen_image_accel.weights import fuse_gate_up
 
 
 class MXFusedProcessor:
@@ -51,7 +53,12 @@ class MXFusedProcessor:
 
 
 def _mx_mlp_forward(self, hidden_states):
-    """SwiGLU whose gate and value projections share one quantized activation."""
+    """SwiGLU whose gate and value projections share one quantized activation.
+
+    With the interleaved gate/up weight (``weights.fuse_gate_up``) and an MXFP8
+    down projection, one GEMM computes both projections and its epilogue writes
+    the down projection's MXFP8 input (the same bytes as the two GEMMs +
+    ``swiglu_quantize``)."""
     lead = hidden_states.shape[:-1]
     if isinstance(hidden_states, Quantized):
         shared = hidden_states
@@ -60,6 +67,11 @@ def _mx_mlp_forward(self, hidden_states):
         shared = quantize(hidden_states.reshape(-1, hidden_states.shape[-1]), tiled=True)
     else:
         return self.out(swiglu(self.gate_layer(hidden_states), self.proj(hidden_states)))
+    gate_up = getattr(self, "_mx_gate_up", None)
+    if gate_up is not None and isinstance(self.out, MXFP8Linear):
+        activated = mx_matmul(shared, gate_up[0], gate_up[1], epilogue="swiglu_quant", weight_tiled=True,
+                              out_tiled=True)
+        return self.out.matmul(activated).view(*lead, -1)
     gate, value = self.gate_layer.matmul(shared), self.proj.matmul(shared)
     if isinstance(self.out, MXFP8Linear):
         activated = swiglu_quantize(gate, value, tiled=True)
@@ -85,6 +97,8 @@ def install_mx_fused_decode(transformer, sage=False):
         eager = block.forward
         block.attn.set_processor(MXFusedProcessor(block.attn.processor, sage=sage))
         block.img_mlp.forward = types.MethodType(_mx_mlp_forward, block.img_mlp)
+        if getattr(block.img_mlp, "_mx_gate_up", None) is None:
+            fuse_gate_up(block.img_mlp)
 
         def forward(*args, _block=block, _eager=eager, **kwargs):
             if kwargs.get("kv_cache_mode") != "cached":

@@ -53,12 +53,20 @@ def install_hot_path(transformer, profile="fused", *, validate=True):
         from qwen_image_accel.optimizations.mxfp8 import quantize_transformer
         skip = os.environ.get("QW21_MXFP8_SKIP_BLOCKS", selected.skip_blocks or "0,31")
         layers = os.environ.get("QW21_MXFP8_LAYERS", "all")
-        config["mxfp8_linears"] = len(quantize_transformer(transformer, skip, layers))
+        weights = os.environ.get("QW21_MXFP8_WEIGHTS", "")
+        if weights:   # pre-quantized weights (weights.save_mxfp8): no quantization at startup
+            from qwen_image_accel.weights import load_mxfp8
+            config["mxfp8_linears"] = len(load_mxfp8(transformer, weights))
+            config["mxfp8_weights"] = weights
+        else:
+            config["mxfp8_linears"] = len(quantize_transformer(transformer, skip, layers))
         config["mxfp8_skipped_blocks"] = skip
         config["mxfp8_layer_selection"] = layers
         config["approximate"] = True
         from qwen_image_accel.optimizations.quantized_decode import install_mx_fused_decode
         install_mx_fused_decode(transformer)
+        config["mxfp8_fused_gate_up"] = sum(getattr(b.img_mlp, "_mx_gate_up", None) is not None
+                                            for b in transformer.transformer_blocks)
     else:
         from qwen_image_accel.optimizations.fusion import install_fused_decode
         install_fused_decode(transformer)
