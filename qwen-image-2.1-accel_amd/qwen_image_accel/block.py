@@ -98,8 +98,9 @@ class MMDiTBlock:
         out-projection's MXFP8 input -- the same bytes as
         ``attention_fn=attention.attention``."""
         b, s, d = h.shape
-        shift1, scale1, g1, shift2, scale2, g2 = (modulation[:, i:i + 1] for i in range(6))
-        gate1, gate2 = g1.tanh(), g2.tanh()
+        shift1, scale1, _, shift2, scale2, _ = (modulation[:, i:i + 1] for i in range(6))
+        gates = modulation[:, 2::3].tanh()                  # tanh(g1), tanh(g2) in one launch
+        gate1, gate2 = gates[:, 0:1], gates[:, 1:2]
         norm = _LayerNorm(d, self.eps)
         hd = d // self.heads
 
