@@ -389,7 +389,5 @@ __device__ __forceinline__ float silu_bf16(float g) {
     return y;
 }
 
-// swiglu element: bf16(bf16(silu(g)) * v) with an fp32 multiply.
-__device__ __forceinline__ float swiglu1(float g, float v) { return rbf(silu_bf16(g) * v); }
 
 }  // namespace qim

@@ -385,8 +385,8 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
             for (int ig = 0; ig < 4; ++ig) {
                 uint8_t *grp = reg + (tl * 8 + ig * 2 + kh) * RGS;  // rows 32tl + 8ig + 4kh + 0..3
                 if constexpr (SWI) {
-                    // swiglu1 on TJ / 2 x 4 values with one exact-path branch;
-                    // the store's bf16 packing is the final rounding.
+                    // bf16(bf16(silu(g)) * v) on TJ / 2 x 4 values with one
+                    // exact-path branch; the store's bf16 packing is the final rounding.
                     constexpr int NS = TJ / 2 * 4;
                     float gs[NS], us[NS], y[NS];
 #pragma unroll
