@@ -238,6 +238,14 @@ static int launch_adaln_rg(const AdaLNArgs &a, hipStream_t st) {
     const dim3 grid((unsigned)a.rows_pad);
     if (nvec % 64 == 0) {
         const int k = nvec / 64;
+        // Vectors per lane: 3 (two waves per row at D = 3072) for the quantizing
+        // kernel, 2 (three waves) for the bf16 one -- measured at D = 3072:
+        // quantizing 15.3 vs 17.0 us (4352 rows), bf16 with residual and gate
+        // 7.92 vs 7.76 us (1280 rows).
+        if (!QUANT && k % 2 == 0 && k / 2 <= ADALN_FULL_WAVES) {
+            hipLaunchKernelGGL((k_adaln<QUANT, 2, true, RG>), grid, dim3(64 * (k / 2)), 0, st, a);
+            return QIM_OK;
+        }
         if (k % 3 == 0 && k / 3 <= ADALN_FULL_WAVES) {
             hipLaunchKernelGGL((k_adaln<QUANT, 3, true, RG>), grid, dim3(64 * (k / 3)), 0, st, a);
             return QIM_OK;
