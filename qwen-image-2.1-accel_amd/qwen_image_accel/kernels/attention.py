@@ -31,20 +31,29 @@ def prepare_attention_inputs(q, k, v, norm_q, norm_k, freqs, cached_k, cached_v)
             or cached_k.shape[2:] != q.shape[2:] or cached_v.shape != cached_k.shape):
         return None
     for t in (q, k, v, cached_k, cached_v):
-        if t.dtype != torch.bfloat16 or not t.is_cuda or t.device != q.device or not t.is_contiguous():
+        if t.dtype != torch.bfloat16 or not t.is_cuda or t.device != q.device:
             return None
+    for t in (cached_k, cached_v):
+        if not t.is_contiguous():
+            return None
+    # q, k, v: contiguous, or column blocks of one fused QKV output -- packed
+    # heads and one token stride shared by the three (the kernel's ldt).
     b, s, h, d = q.shape
+    ldt = q.stride(1)
+    for t in (q, k, v):
+        if t.stride() != (s * ldt, ldt, d, 1):
+            return None
     if not (_norm_ok(norm_q, d, q.device) and _norm_ok(norm_k, d, q.device)):
         return None
     p = cached_k.shape[1]
-    oq = torch.empty_like(q)
+    oq = torch.empty((b, s, h, d), device=q.device, dtype=q.dtype)
     ok = torch.empty((b, s + p, h, d), device=q.device, dtype=q.dtype)
     ov = torch.empty_like(ok)
     f = torch.view_as_real(freqs)
     _native.call("qim_qk_norm_rope_pack", _native.ptr(q), _native.ptr(k), _native.ptr(v),
                  _native.ptr(cached_k) if p else None, _native.ptr(cached_v) if p else None,
                  _native.ptr(norm_q.weight), _native.ptr(norm_k.weight), _native.ptr(f),
-                 _native.ptr(oq), _native.ptr(ok), _native.ptr(ov), b, s, p, h, d, h * d,
+                 _native.ptr(oq), _native.ptr(ok), _native.ptr(ov), b, s, p, h, d, ldt,
                  float(norm_q.eps), float(norm_k.eps), _native.stream(q.device))
     return oq, ok, ov
 

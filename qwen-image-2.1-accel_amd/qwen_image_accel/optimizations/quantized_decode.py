@@ -18,7 +18,7 @@ from qwen_image_accel.kernels.layernorm import layer_norm_scale
 from qwen_image_accel.kernels.mxfp8 import Quantized, quantize
 from qwen_image_accel.optimizations.fusion import _attend, modulation_values
 from qwen_image_accel.optimizations.mxfp8 import MXFP8Linear
-from qwen_image_accel.weights import fuse_gate_up
+from qwen_image_accel.weights import fuse_gate_up, fuse_qkv
 
 
 class MXFusedProcessor:
@@ -39,7 +39,17 @@ class MXFusedProcessor:
             return self.native(attn, hidden_states, attention_mask, rotary_emb, layer_cache,
                                kv_cache_mode, cache_write_slice, segments, key_valid)
         projections = (attn.to_q, attn.to_k, attn.to_v)
-        if isinstance(hidden_states, Quantized):
+        qkv = getattr(attn, "_mx_qkv", None)
+        if qkv is not None and (isinstance(hidden_states, Quantized) or hidden_states.is_contiguous()):
+            # One GEMM for the three projections (weights.fuse_qkv); Q, K, V are
+            # column blocks of its output, which the norm + RoPE + pack reads in place.
+            shared = hidden_states if isinstance(hidden_states, Quantized) else \
+                quantize(hidden_states.reshape(-1, hidden_states.shape[-1]), tiled=True)
+            lead = hidden_states.shape[:-1]
+            out = mx_matmul(shared, qkv[0], qkv[1], weight_tiled=True).view(*lead, -1)
+            d = out.shape[-1] // 3
+            q, k, v = (out[..., i * d:(i + 1) * d].unflatten(-1, (attn.heads, -1)) for i in range(3))
+        elif isinstance(hidden_states, Quantized):
             # The block's LayerNorm already emitted FP8; no BF16 tensor exists.
             lead = hidden_states.shape[:-1]
             q, k, v = (p.matmul(hidden_states).view(*lead, attn.heads, -1) for p in projections)
@@ -99,6 +109,8 @@ def install_mx_fused_decode(transformer, sage=False):
         block.img_mlp.forward = types.MethodType(_mx_mlp_forward, block.img_mlp)
         if getattr(block.img_mlp, "_mx_gate_up", None) is None:
             fuse_gate_up(block.img_mlp)
+        if getattr(block.attn, "_mx_qkv", None) is None:
+            fuse_qkv(block.attn)
 
         def forward(*args, _block=block, _eager=eager, **kwargs):
             if kwargs.get("kv_cache_mode") != "cached":

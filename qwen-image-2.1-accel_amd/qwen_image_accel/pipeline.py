@@ -67,6 +67,8 @@ def install_hot_path(transformer, profile="fused", *, validate=True):
         install_mx_fused_decode(transformer)
         config["mxfp8_fused_gate_up"] = sum(getattr(b.img_mlp, "_mx_gate_up", None) is not None
                                             for b in transformer.transformer_blocks)
+        config["mxfp8_fused_qkv"] = sum(getattr(b.attn, "_mx_qkv", None) is not None
+                                        for b in transformer.transformer_blocks)
     else:
         from qwen_image_accel.optimizations.fusion import install_fused_decode
         install_fused_decode(transformer)

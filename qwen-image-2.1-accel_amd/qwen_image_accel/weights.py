@@ -13,8 +13,10 @@ projections as two GEMMs whose bf16 outputs ``swiglu_quantize`` reads back
   scales gives exactly the bytes of quantizing the interleaved bf16 weight; no
   requantization.  The decode MLP then runs one GEMM whose epilogue writes the
   down projection's MXFP8 input (no [M, 2F] bf16 round trip).
+* ``fuse_qkv`` stacks the Q, K and V projections' quantized weights into one
+  (3N, K) weight: the decode path's three projection GEMMs become one.
 * ``save_mxfp8`` / ``load_mxfp8`` keep every converted linear's codes (tiled
-  layout), scales and bias, and the interleaved gate/up weights, in a
+  layout), scales and bias, and the fused gate/up and QKV weights, in a
   safetensors file; loading replaces the same linears without quantizing.
 """
 import json
@@ -76,6 +78,26 @@ def fuse_gate_up(mlp):
     return True
 
 
+def fuse_qkv(attn):
+    """Attach the Q, K and V projections of an attention module as one MXFP8
+    weight (``attn._mx_qkv``: rows Q, then K, then V), so that the decode
+    path runs one GEMM instead of three.  Needs three MXFP8 linears of the
+    same (N, K) with N % 256 == 0: the tiled codes of each are whole 256-row
+    super-blocks and its swizzled scales whole 128-row tiles, so both
+    concatenate as flat byte arrays.  Returns whether it did."""
+    ps = [getattr(attn, n, None) for n in ("to_q", "to_k", "to_v")]
+    if not all(isinstance(p, MXFP8Linear) for p in ps):
+        return False
+    n, k = ps[0].out_features, ps[0].in_features
+    if any((p.out_features, p.in_features) != (n, k) for p in ps) or n % 256:
+        return False
+    attn._mx_qkv = (torch.cat([p.weight_tiled for p in ps], 0), torch.cat([p.weight_scale for p in ps], 0))
+    return True
+
+
+_FUSED = ("_mx_gate_up", "_mx_qkv")
+
+
 def _modules(transformer):
     """(path, module) over the DiT blocks, paths as quantize_transformer names
     them ("transformer_blocks.<i>.<name>")."""
@@ -109,13 +131,14 @@ def save_mxfp8(transformer, path):
             tensors[f"{name}.bias"] = m.bias.cpu().contiguous()
         layers[name] = [m.in_features, m.out_features]
     for name, mod in _modules(transformer):
-        gu = getattr(mod, "_mx_gate_up", None)
-        if gu is not None:
-            tensors[f"{name}._mx_gate_up.codes"] = gu[0].view(torch.uint8).cpu().contiguous()
-            tensors[f"{name}._mx_gate_up.scales"] = gu[1].view(torch.uint8).cpu().contiguous()
-            fused.append(name)
+        for attr in _FUSED:
+            w = getattr(mod, attr, None)
+            if w is not None:
+                tensors[f"{name}.{attr}.codes"] = w[0].view(torch.uint8).cpu().contiguous()
+                tensors[f"{name}.{attr}.scales"] = w[1].view(torch.uint8).cpu().contiguous()
+                fused.append(f"{name}.{attr}")
     meta = {"format": FORMAT, "version": str(VERSION), "swiglu_group": str(_native.SWIGLU_GROUP),
-            "layers": json.dumps(layers), "fused_gate_up": json.dumps(fused)}
+            "layers": json.dumps(layers), "fused": json.dumps(fused)}
     save_file(tensors, path, metadata=meta)
     return sorted(layers)
 
@@ -143,13 +166,17 @@ def load_mxfp8(transformer, path, device=None):
                                              f.get_tensor(f"{name}.scales").to(dev), bias)
             _set(transformer, name, new)
             loaded.append(name)
-        for name in json.loads(meta["fused_gate_up"]):
+        for key in json.loads(meta["fused"]):
+            name, _, attr = key.rpartition(".")
+            if attr not in _FUSED:
+                raise ValueError(f"{path}: unknown fused weight {key}")
             mod = _resolve(transformer, name)
-            gate = mod.gate_layer
-            dev = gate.weight_tiled.device
-            mod._mx_gate_up = (f.get_tensor(f"{name}._mx_gate_up.codes").to(dev).view(gate.weight_tiled.dtype),
-                               f.get_tensor(f"{name}._mx_gate_up.scales").to(dev).view(gate.weight_scale.dtype))
+            ref = mod.gate_layer if attr == "_mx_gate_up" else mod.to_q
+            dev = ref.weight_tiled.device
+            setattr(mod, attr, (f.get_tensor(f"{key}.codes").to(dev).view(ref.weight_tiled.dtype),
+                                f.get_tensor(f"{key}.scales").to(dev).view(ref.weight_scale.dtype)))
     return loaded
 
 
-__all__ = ["unswizzle_scales", "swizzle_scales", "interleave_quantized", "fuse_gate_up", "save_mxfp8", "load_mxfp8"]
+__all__ = ["unswizzle_scales", "swizzle_scales", "interleave_quantized", "fuse_gate_up", "fuse_qkv", "save_mxfp8",
+           "load_mxfp8"]

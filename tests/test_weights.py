@@ -50,6 +50,20 @@ def test_interleaved_gate_up_equals_quantized_interleave(f, k):
     assert np.array_equal(u8(scales), ref_scales)
 
 
+def test_fused_qkv_equals_quantized_concatenation():
+    """Q, K, V weights stacked as one (3N, K) MXFP8 weight: the bytes of
+    quantizing the stacked bf16 weight."""
+    g = torch.Generator().manual_seed(9)
+    ws = [(torch.randn(256, 384, generator=g) * 0.05).to(torch.bfloat16) for _ in range(3)]
+    ws[1][7, 100:] *= 300
+    attn = torch.nn.Module()
+    attn.to_q, attn.to_k, attn.to_v = (oracle_linear(w) for w in ws)
+    assert weights.fuse_qkv(attn)
+    ref_codes, ref_scales = O.mx_quantize(bits(torch.cat(ws, 0)))
+    assert np.array_equal(u8(mxfp8.untile_codes(attn._mx_qkv[0])), ref_codes)
+    assert np.array_equal(u8(attn._mx_qkv[1]), ref_scales)
+
+
 def _quantized_fake(seed=0):
     t = fq.make_transformer(dim=256, heads=2, ffn=512, seed=seed)
     for b in t.transformer_blocks:
@@ -59,6 +73,7 @@ def _quantized_fake(seed=0):
             lin = b.get_submodule(name)
             setattr(b.get_submodule(parent), leaf, oracle_linear(lin.weight.detach().to(torch.bfloat16)))
         assert weights.fuse_gate_up(b.img_mlp)
+        assert weights.fuse_qkv(b.attn)
     return t
 
 
@@ -78,6 +93,8 @@ def test_save_and_load_prequantized_weights(tmp_path):
     for i in range(2):
         ga, gb = src.transformer_blocks[i].img_mlp._mx_gate_up, dst.transformer_blocks[i].img_mlp._mx_gate_up
         assert np.array_equal(u8(ga[0]), u8(gb[0])) and np.array_equal(u8(ga[1]), u8(gb[1]))
+        qa, qb = src.transformer_blocks[i].attn._mx_qkv, dst.transformer_blocks[i].attn._mx_qkv
+        assert np.array_equal(u8(qa[0]), u8(qb[0])) and np.array_equal(u8(qa[1]), u8(qb[1]))
 
 
 def test_load_rejects_other_files_and_shapes(tmp_path):
@@ -109,24 +126,27 @@ def _profile_out(dev, t, inputs):
 @pytest.mark.gpu
 def test_mxfp8_profile_fused_gate_up_and_prequantized_weights(dev, monkeypatch, tmp_path):
     """The mxfp8 profile's decode MLP as one interleaved gate/up GEMM with the
-    SwiGLU -> MXFP8 epilogue equals, byte for byte, the two GEMMs +
-    swiglu_quantize; and a transformer whose weights load from a
-    save_mxfp8 file (no quantization) gives the same output again."""
+    SwiGLU -> MXFP8 epilogue, and its Q/K/V projections as one GEMM, equal,
+    byte for byte, the separate GEMMs (+ swiglu_quantize); and a transformer
+    whose weights load from a save_mxfp8 file (no quantization) gives the
+    same output again."""
     print("[case] mxfp8 fused gate/up + prequantized weights", flush=True)
     monkeypatch.setenv("QW21_MXFP8_SKIP_BLOCKS", "")
     base = fq.make_transformer(dim=512, heads=4, ffn=1024, device=dev)
     inputs = fq.make_inputs(dim=512, heads=4, tokens=200, prefix=37, batch=1, device=dev)
     t_fused, t_plain, t_loaded = copy.deepcopy(base), copy.deepcopy(base), copy.deepcopy(base)
     cfg, fused = _profile_out(dev, t_fused, inputs)
-    assert cfg["mxfp8_fused_gate_up"] == 2
+    assert cfg["mxfp8_fused_gate_up"] == 2 and cfg["mxfp8_fused_qkv"] == 2
     with monkeypatch.context() as m:
         m.setattr(quantized_decode, "fuse_gate_up", lambda mlp: False)
+        m.setattr(quantized_decode, "fuse_qkv", lambda attn: False)
         cfg_p, plain = _profile_out(dev, t_plain, inputs)
-    assert cfg_p["mxfp8_fused_gate_up"] == 0
+    assert cfg_p["mxfp8_fused_gate_up"] == 0 and cfg_p["mxfp8_fused_qkv"] == 0
     assert torch.equal(fused, plain)
     path = str(tmp_path / "w.safetensors")
     weights.save_mxfp8(t_fused, path)
     monkeypatch.setenv("QW21_MXFP8_WEIGHTS", path)
     cfg_l, loaded = _profile_out(dev, t_loaded, inputs)
     assert cfg_l["mxfp8_weights"] == path and cfg_l["mxfp8_linears"] == 14 and cfg_l["mxfp8_fused_gate_up"] == 2
+    assert cfg_l["mxfp8_fused_qkv"] == 2
     assert torch.equal(loaded, fused)
