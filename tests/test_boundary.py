@@ -142,3 +142,34 @@ def test_mxfp8_default_skip_blocks(dev):
     cfg, used, err = _run_profile(dev, "mxfp8")
     assert cfg["mxfp8_linears"] == 7 and cfg["mxfp8_skipped_blocks"] == "0,31"
     assert err < 5e-2, err
+
+
+def test_attention_backend_env_is_validated(monkeypatch):
+    from qwen_image_accel.optimizations import attention_call
+    monkeypatch.setenv("QW21_ATTENTION_BACKEND", "flash")
+    x = torch.zeros(1, 4, 2, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="QW21_ATTENTION_BACKEND"):
+        attention_call.attention(x, x, x)
+
+
+@pytest.mark.gpu
+def test_mxfp8_profile_with_qim_attention_backend(dev, monkeypatch):
+    """QW21_ATTENTION_BACKEND=qim: the decode attention runs on qim_attention;
+    the block output stays within the attention bar of the default path."""
+    print("[case] boundary mxfp8 + qim attention", flush=True)
+    monkeypatch.setenv("QW21_MXFP8_SKIP_BLOCKS", "")
+    _, used0, _ = _run_profile(dev, "mxfp8")
+    assert "qim_attention" not in used0
+    t = fq.make_transformer(dim=512, heads=4, ffn=1024, device=dev)
+    ref_t = copy.deepcopy(t)
+    inputs = fq.make_inputs(dim=512, heads=4, tokens=200, prefix=37, batch=1, device=dev)
+    with torch.no_grad():
+        pipeline.install_hot_path(ref_t, "mxfp8", validate=False)
+        want = _cached(ref_t, inputs)
+        monkeypatch.setenv("QW21_ATTENTION_BACKEND", "qim")
+        before = dict(_native.calls)
+        pipeline.install_hot_path(t, "mxfp8", validate=False)
+        got = _cached(t, inputs)
+    torch.cuda.synchronize()
+    assert _native.calls.get("qim_attention", 0) > before.get("qim_attention", 0)
+    assert rel_fro(got.float().cpu().numpy(), want.float().cpu().numpy()) < 1e-2
