@@ -26,11 +26,17 @@ def _qim_applies(q, k, v, attention_mask):
                and t.stride(0) == t.shape[1] * t.stride(1) for t in (q, k, v))
 
 
-def attention(q, k, v, attention_mask=None, processor=None):
+def qim_backend(q, k, v, attention_mask=None):
+    """Whether this call goes to qim_attention (QW21_ATTENTION_BACKEND=qim and
+    the inputs fit it)."""
     backend = os.environ.get("QW21_ATTENTION_BACKEND", "dispatch")
     if backend not in BACKENDS:
         raise ValueError(f"QW21_ATTENTION_BACKEND={backend!r}: choose from {BACKENDS}")
-    if backend == "qim" and _qim_applies(q, k, v, attention_mask):
+    return backend == "qim" and _qim_applies(q, k, v, attention_mask)
+
+
+def attention(q, k, v, attention_mask=None, processor=None):
+    if qim_backend(q, k, v, attention_mask):
         from qwen_image_accel.kernels.attention import attention as qim_attention
         return qim_attention(q, k, v)
     try:

@@ -11,7 +11,7 @@ import torch
 from qwen_image_accel.kernels.attention import prepare_attention_inputs
 from qwen_image_accel.kernels.elementwise import residual, rope_qk
 from qwen_image_accel.kernels.layernorm import layer_norm_scale
-from qwen_image_accel.optimizations.attention_call import attention
+from qwen_image_accel.optimizations.attention_call import attention, qim_backend
 
 
 class FusedRopeProcessor:
@@ -45,8 +45,16 @@ def _attend(processor, attn, q, k, v, attention_mask, rotary_emb, layer_cache):
         if rotary_emb is not None:
             q, k = _rope(q, k, rotary_emb)
         k, v = torch.cat([cached_k, k], dim=1), torch.cat([cached_v, v], dim=1)
+    out_proj = attn.to_out[0]
+    if getattr(out_proj, "weight_tiled", None) is not None and qim_backend(q, k, v, attention_mask):
+        # MXFP8 out-projection after this build's attention core: the core
+        # writes the projection's MXFP8 input itself (qim_attention_mxfp8),
+        # the same bytes MXFP8Linear.forward would quantize.
+        from qwen_image_accel.kernels.attention import attention_mxfp8
+        lead = q.shape[:2]
+        return attn.to_out[1](out_proj.matmul(attention_mxfp8(q, k, v)).view(*lead, -1))
     result = attention(q, k, v, attention_mask, getattr(processor, "native", None))
-    return attn.to_out[1](attn.to_out[0](result.flatten(2, 3).to(q.dtype)))
+    return attn.to_out[1](out_proj(result.flatten(2, 3).to(q.dtype)))
 
 
 def _rope(q, k, freqs):

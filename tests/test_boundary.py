@@ -154,8 +154,10 @@ def test_attention_backend_env_is_validated(monkeypatch):
 
 @pytest.mark.gpu
 def test_mxfp8_profile_with_qim_attention_backend(dev, monkeypatch):
-    """QW21_ATTENTION_BACKEND=qim: the decode attention runs on qim_attention;
-    the block output stays within the attention bar of the default path."""
+    """QW21_ATTENTION_BACKEND=qim: the decode attention runs on this build's
+    core, which also writes the MXFP8 out-projection's input
+    (qim_attention_mxfp8); the block output stays within the attention bar of
+    the default path."""
     print("[case] boundary mxfp8 + qim attention", flush=True)
     monkeypatch.setenv("QW21_MXFP8_SKIP_BLOCKS", "")
     _, used0, _ = _run_profile(dev, "mxfp8")
@@ -171,5 +173,6 @@ def test_mxfp8_profile_with_qim_attention_backend(dev, monkeypatch):
         pipeline.install_hot_path(t, "mxfp8", validate=False)
         got = _cached(t, inputs)
     torch.cuda.synchronize()
-    assert _native.calls.get("qim_attention", 0) > before.get("qim_attention", 0)
+    # the out-projection is MXFP8: the core writes its input (qim_attention_mxfp8)
+    assert _native.calls.get("qim_attention_mxfp8", 0) > before.get("qim_attention_mxfp8", 0)
     assert rel_fro(got.float().cpu().numpy(), want.float().cpu().numpy()) < 1e-2
