@@ -68,9 +68,12 @@ def interleave_quantized(gate, up, group=_native.SWIGLU_GROUP):
 def fuse_gate_up(mlp):
     """Attach the interleaved gate/up weight to a SwiGLU MLP whose gate and
     value projections are MXFP8 (``mlp._mx_gate_up``, used by the decode MLP).
-    Returns whether it did.  Needs F % 256 == 0 (the SwiGLU epilogue's N)."""
+    Returns whether it did.  Needs F % 256 == 0 (the SwiGLU epilogue's N) and
+    bias-free projections."""
     gate, up = getattr(mlp, "gate_layer", None), getattr(mlp, "proj", None)
     if not (isinstance(gate, MXFP8Linear) and isinstance(up, MXFP8Linear)) or gate.out_features % 256:
+        return False
+    if gate.bias is not None or up.bias is not None:  # the SwiGLU epilogue adds no bias
         return False
     if (up.out_features, up.in_features) != (gate.out_features, gate.in_features):
         return False
@@ -86,7 +89,7 @@ def fuse_qkv(attn):
     super-blocks and its swizzled scales whole 128-row tiles, so both
     concatenate as flat byte arrays.  Returns whether it did."""
     ps = [getattr(attn, n, None) for n in ("to_q", "to_k", "to_v")]
-    if not all(isinstance(p, MXFP8Linear) for p in ps):
+    if not all(isinstance(p, MXFP8Linear) and p.bias is None for p in ps):  # one plain GEMM: no biases
         return False
     n, k = ps[0].out_features, ps[0].in_features
     if any((p.out_features, p.in_features) != (n, k) for p in ps) or n % 256:

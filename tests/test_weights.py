@@ -64,6 +64,20 @@ def test_fused_qkv_equals_quantized_concatenation():
     assert np.array_equal(u8(attn._mx_qkv[1]), ref_scales)
 
 
+def test_fusions_skip_biased_projections():
+    g = torch.Generator().manual_seed(3)
+    w = (torch.randn(256, 256, generator=g) * 0.05).to(torch.bfloat16)
+    attn, mlp = torch.nn.Module(), torch.nn.Module()
+    attn.to_q, attn.to_k, attn.to_v = oracle_linear(w), oracle_linear(w), oracle_linear(w)
+    attn.to_k.bias = torch.zeros(256, dtype=torch.bfloat16)
+    mlp.gate_layer, mlp.proj = oracle_linear(w), oracle_linear(w)
+    mlp.proj.bias = torch.zeros(256, dtype=torch.bfloat16)
+    assert not weights.fuse_qkv(attn) and getattr(attn, "_mx_qkv", None) is None
+    assert not weights.fuse_gate_up(mlp) and getattr(mlp, "_mx_gate_up", None) is None
+    with pytest.raises(ValueError, match="does not match"):
+        mx.MXFP8Linear.from_quantized(256, 512, attn.to_q.weight_tiled, attn.to_q.weight_scale)
+
+
 def _quantized_fake(seed=0):
     t = fq.make_transformer(dim=256, heads=2, ffn=512, seed=seed)
     for b in t.transformer_blocks:
