@@ -90,8 +90,32 @@ __global__ __launch_bounds__(FULL ? 64 * ADALN_FULL_WAVES : 64 * ADALN_MAX_WAVES
         const int j = tid + nthr * i;
         const bool ok = FULL || j < nvec;
         xv[i] = ok ? ld_nt(xr + j) : zero;
-        sv[i] = ok ? sc[j] : zero;
     }
+    // The per-batch scale and shift vectors (L2-resident, shared by every row)
+    // are loaded with x in the bf16-output kernel and after the statistics in
+    // the quantizing one, where the shorter live range lowers the register
+    // count from 120 to 96 (5 waves per SIMD instead of 4; 4352 rows:
+    // 15.4 -> 14.9 us; the bf16 kernel measured no gain).
+    constexpr bool LATE = QUANT;
+    auto load_scale_shift = [&]() {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int j = tid + nthr * i;
+            sv[i] = (FULL || j < nvec) ? sc[j] : zero;
+        }
+        if (p.shift) {
+            const uint4 *sh = reinterpret_cast<const uint4 *>(p.shift + (int64_t)b * p.D);
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+                const int j = tid + nthr * i;
+                hv[i] = (FULL || j < nvec) ? sh[j] : neg0;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < NV; ++i) hv[i] = neg0;
+        }
+    };
+    if constexpr (!LATE) load_scale_shift();
     if (RG && p.res) {
         const uint4 *rr = reinterpret_cast<const uint4 *>(p.res + row * p.D);
 #pragma unroll
@@ -102,17 +126,6 @@ __global__ __launch_bounds__(FULL ? 64 * ADALN_FULL_WAVES : 64 * ADALN_MAX_WAVES
     } else {
 #pragma unroll
         for (int i = 0; i < NV; ++i) rv[i] = neg0;
-    }
-    if (p.shift) {
-        const uint4 *sh = reinterpret_cast<const uint4 *>(p.shift + (int64_t)b * p.D);
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            const int j = tid + nthr * i;
-            hv[i] = (FULL || j < nvec) ? sh[j] : neg0;
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < NV; ++i) hv[i] = neg0;
     }
     if (RG && p.gate) {
         const uint4 *ga = reinterpret_cast<const uint4 *>(p.gate + (int64_t)b * p.D);
@@ -163,6 +176,7 @@ __global__ __launch_bounds__(FULL ? 64 * ADALN_FULL_WAVES : 64 * ADALN_MAX_WAVES
     const float rstd = rstd_of((float)(ss / (double)p.D), p.eps);
     // t1 = bf16(scale + 1) with add_one, else scale (+ -0 leaves it unchanged).
     const float scale_add = (p.flags & QIM_ADALN_ADD_ONE) ? 1.0f : -0.0f;
+    if constexpr (LATE) load_scale_shift();
 
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
