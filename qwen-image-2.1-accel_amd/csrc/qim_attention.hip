@@ -573,7 +573,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
 // Combine the chunks of each tail item from their normalised rows
 // R_c = O_c / l_c: O = sum_c w_c R_c / sum_c w_c with w_c = 2^(m_c - M) l_c,
-// M = max_c m_c.  One thread per (item, query, 8 d).
+// M = max_c m_c (accumulated with a running max).  One thread per (item,
+// query, 8 d).
 __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs p) {
     const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int dg = (int)(g & 15), ql = (int)((g >> 4) & (ATT_BQ - 1));
@@ -583,22 +584,24 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs p) {
     const int qblk = item % p.nq, h = (item / p.nq) % p.H, b = item / (p.nq * p.H);
     const int qi = qblk * ATT_BQ + ql;
     if (qi >= p.S) return;
+    // One pass, rescaling the running sums when the max grows, so that each
+    // chunk's loads do not wait for the previous chunks' arithmetic.
     const int nc = p.nsplit;
-    float M = -__builtin_inff();
-    for (int c = 0; c < nc; ++c) {
-        const float m = p.part_ml[((int64_t)(ti * p.nsplit + c) * ATT_BQ + ql) * 2];
-        M = m > M ? m : M;
-    }
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, wsum = 0.f;
+    float M = -__builtin_inff(), wsum = 0.f;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll 2
     for (int c = 0; c < nc; ++c) {
         const int64_t tc = (int64_t)(ti * p.nsplit + c);
         const float2 ml = *reinterpret_cast<const float2 *>(p.part_ml + (tc * ATT_BQ + ql) * 2);
-        const float w = __builtin_amdgcn_exp2f(ml.x - M) * ml.y;
-        wsum += w;
         float r[8];
         unpack8(*reinterpret_cast<const uint4 *>(p.part_o + (tc * ATT_BQ + ql) * ATT_D + dg * 8), r);
+        const float Mn = ml.x > M ? ml.x : M;
+        const float sc = __builtin_amdgcn_exp2f(M - Mn);  // 0 on the first chunk (M = -inf)
+        const float w = __builtin_amdgcn_exp2f(ml.x - Mn) * ml.y;
+        wsum = wsum * sc + w;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] += w * r[e];
+        for (int e = 0; e < 8; ++e) acc[e] = acc[e] * sc + w * r[e];
+        M = Mn;
     }
     const float inv = 1.0f / wsum;
     if (p.qcodes) {
