@@ -69,6 +69,23 @@ struct GemmArgs {
     int64_t vt_nkb;
 };
 
+// qim_mxfp8_gemm_qk_norm_rope_vt: the QK-norm + RoPE epilogue whose V columns
+// leave as V^T tiles (an instantiation of its own, so the plain QKV kernel
+// carries none of it).  Its outputs are read next by the attention core, so
+// it stores through the caches (block @1024^2 with attention: 881 -> 874 us)
+// where every other epilogue streams its output past them.
+constexpr int EPI_QKV_VT = 6;
+template <int EPI>
+constexpr bool is_qk_epi() { return EPI == QIM_EPI_QK_NORM_ROPE || EPI == EPI_QKV_VT; }
+
+template <typename V>
+__device__ __forceinline__ void st_out(bool cached, void *ptr, const V &v) {
+    if (cached)
+        *reinterpret_cast<V *>(ptr) = v;
+    else
+        st_nt(ptr, v);
+}
+
 __device__ __forceinline__ int kswz(int row) { return mx_chunk_swizzle(row); }
 // LDS byte offset of logical 16-byte chunk c of tile row `row` (64-byte rows).
 __device__ __forceinline__ int lds_off(int row, int c) { return row * BK + ((c ^ kswz(row)) << 4); }
@@ -355,7 +372,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
     // 32-lane group over all banks) and leave as V^T tiles.
     [[maybe_unused]] constexpr int VT_COL = 136;
     static_assert(W * VT_COL <= 16 * RGS, "V^T staging fits the wave's region");
-    const bool vtw = EPI == QIM_EPI_QK_NORM_ROPE && p.vt && col0 >= p.qk_cols;
+    const bool vtw = EPI == EPI_QKV_VT && col0 >= p.qk_cols;
     float bias[TJ] = {};
     if constexpr (EPI == QIM_EPI_BIAS) {
 #pragma unroll
@@ -444,7 +461,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
                     const int c = pc ^ ((d >> 1) & 7), k0 = 16 * (c >> 1) + 4 * (c & 1);
                     const uint2 lo = *reinterpret_cast<const uint2 *>(reg + dl * VT_COL + k0 * 2);
                     const uint2 hi = *reinterpret_cast<const uint2 *>(reg + dl * VT_COL + (k0 + 8) * 2);
-                    st_nt(tile + d * 64 + pc * 8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+                    *reinterpret_cast<uint4 *>(tile + d * 64 + pc * 8) = make_uint4(lo.x, lo.y, hi.x, hi.y);
                 }
             }
             continue;
@@ -471,7 +488,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
                 for (int r = 0; r < 4; ++r) rowv[r] = make_uint4(w[r][0], w[r][1], w[r][2], w[r][3]);
             }
             const int64_t col = col0 + cl * 8;
-            if constexpr (EPI == QIM_EPI_QK_NORM_ROPE) {
+            if constexpr (is_qk_epi<EPI>()) {
                 // Q and K head columns: RMSNorm + RoPE of each row's 128-wide
                 // head, as k_norm_rope computes it on the stored output.  A
                 // wave holds W columns of the head; with W = 64 (quarter tiles)
@@ -544,7 +561,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
                         for (int t = 0; t < 8; ++t) z[t] = h[t] + rbf(gg[t] * y[t]);
                         o = pack8(z);
                     }
-                    st_nt(reinterpret_cast<uint16_t *>(p.out) + grow * p.ldo + col, o);
+                    st_out(EPI == EPI_QKV_VT, reinterpret_cast<uint16_t *>(p.out) + grow * p.ldo + col, o);
                 }
             }
         }
@@ -834,7 +851,8 @@ static int gemm_run(const void *aq, const void *as, const void *bq, const void *
         case QIM_EPI_QK_NORM_ROPE:
             QIM_REQUIRE(qk, QIM_ERR_ARG, "qim_mxfp8_gemm: the QK epilogue is qim_mxfp8_gemm_qk_norm_rope's");
             QIM_REQUIRE(ldo >= N, QIM_ERR_LAYOUT, "qim_mxfp8_gemm: ldo=%lld < N", (long long)ldo);
-            rc = launch_gemm<QIM_EPI_QK_NORM_ROPE>(a, tiles, as_stream(stream));
+            rc = qk->vt ? launch_gemm<EPI_QKV_VT>(a, tiles, as_stream(stream))
+                        : launch_gemm<QIM_EPI_QK_NORM_ROPE>(a, tiles, as_stream(stream));
             break;
         default:
             return fail(QIM_ERR_ARG, "qim_mxfp8_gemm: unknown epilogue %d", epilogue);
