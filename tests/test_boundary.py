@@ -176,3 +176,20 @@ def test_mxfp8_profile_with_qim_attention_backend(dev, monkeypatch):
     # the out-projection is MXFP8: the core writes its input (qim_attention_mxfp8)
     assert _native.calls.get("qim_attention_mxfp8", 0) > before.get("qim_attention_mxfp8", 0)
     assert rel_fro(got.float().cpu().numpy(), want.float().cpu().numpy()) < 1e-2
+
+
+def test_qim_attention_backend_applies_only_where_it_can(monkeypatch):
+    """QW21_ATTENTION_BACKEND=qim routes only unmasked bf16 CUDA calls with head
+    dim 128 and packed heads; everything else keeps the reference's dispatch."""
+    from qwen_image_accel.optimizations import attention_call
+    x = torch.zeros(1, 4, 2, 128, dtype=torch.bfloat16)
+    monkeypatch.delenv("QW21_ATTENTION_BACKEND", raising=False)
+    assert not attention_call.qim_backend(x, x, x)
+    monkeypatch.setenv("QW21_ATTENTION_BACKEND", "qim")
+    assert not attention_call.qim_backend(x, x, x)                      # CPU tensors
+    assert not attention_call._qim_applies(x.float(), x.float(), x.float(), None)
+    assert not attention_call._qim_applies(x, x, x, torch.ones(1, 1, 4, 4, dtype=torch.bool))
+    y = torch.zeros(1, 4, 2, 64, dtype=torch.bfloat16)
+    assert not attention_call._qim_applies(y, y, y, None)                # head dim 64
+    out = attention_call.attention(x, x, x)                              # falls back to SDPA on the CPU
+    assert out.shape == x.shape and out.dtype == x.dtype
