@@ -23,6 +23,7 @@
 // 16-byte chunk c of row d at chunk c ^ ((d >> 1) & 7) (conflict-free reads of
 // 16 lanes with consecutive d).  K is loaded straight from the K tensor, with
 // chunk c of key r at chunk c ^ (r & 15) in LDS.
+#include "qim_attention.h"
 #include "qim_device.h"
 #include "qim_runtime.h"
 
@@ -651,15 +652,11 @@ using namespace qim;
 // fp32 (m, l): 66 KiB per chunk.  (At S = T = 16640 and 24 heads the 24 tail
 // items run as 10 chunks each, ~10 % faster; at S = T = 4352 the 152 tail
 // items of one image run as 3 chunks each, ~1 % faster.)
+namespace qim {
+
 constexpr int ATT_MIN_CHUNK = 8;
 
-struct AttPlan {
-    int64_t nfull, ntail, nsplit, kbc;
-    int64_t vt_bytes, part_o_bytes, part_ml_bytes;
-    int64_t total() const { return vt_bytes + part_o_bytes + part_ml_bytes; }
-};
-
-static AttPlan att_plan(int64_t B, int64_t S, int64_t T, int64_t H) {
+AttPlan att_plan(int64_t B, int64_t S, int64_t T, int64_t H) {
     const int64_t nq = (S + ATT_BQ - 1) / ATT_BQ, nkb = (T + ATT_KB - 1) / ATT_KB, W = B * H * nq;
     const int64_t C = device_cus() > 0 ? device_cus() : 256;
     AttPlan pl{W, 0, 1, nkb, B * H * nkb * ATT_TILE, 0, 0};
@@ -689,10 +686,11 @@ static AttPlan att_plan(int64_t B, int64_t S, int64_t T, int64_t H) {
     return pl;
 }
 
-// The checks and launches both entry points share.  Output: bf16 rows of o
-// (ldo elements apart), or MXFP8 codes and scales when qcodes is set.  v null:
-// the workspace already holds V^T (qim_mxfp8_gemm_qk_norm_rope_vt), T % 64 == 0.
-static int attention_run(const char *who, const void *q, int64_t ldq, const void *k, int64_t ldk, const void *v,
+// The checks and launches the attention entry points share.  Output: bf16 rows
+// of o (ldo elements apart), or MXFP8 codes and scales when qcodes is set.
+// v null: the workspace already holds V^T (qim_mxfp8_gemm_qk_norm_rope_vt),
+// T % 64 == 0.
+int attention_run(const char *who, const void *q, int64_t ldq, const void *k, int64_t ldk, const void *v,
                          int64_t ldv, void *o, int64_t ldo, void *qcodes, void *qscales, int tiled, void *workspace,
                          int64_t workspace_bytes, int64_t B, int64_t S, int64_t T, int64_t H, int64_t D, float scale,
                          void *stream) {
@@ -766,6 +764,8 @@ static int attention_run(const char *who, const void *q, int64_t ldq, const void
     }
     return check_launch(who);
 }
+
+}  // namespace qim
 
 extern "C" int qim_attention(const void *q, int64_t ldq, const void *k, int64_t ldk, const void *v, int64_t ldv,
                              void *o, int64_t ldo, void *workspace, int64_t workspace_bytes, int64_t B, int64_t S,
