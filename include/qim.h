@@ -228,6 +228,22 @@ int qim_attention_mxfp8(const void *q, int64_t ldq, const void *k, int64_t ldk, 
                         void *codes, void *scales, int tiled, void *workspace, int64_t workspace_bytes,
                         int64_t B, int64_t S, int64_t T, int64_t H, int64_t D, float scale, void *stream);
 
+/* qim_attention without a workspace argument and without allocating: the
+ * workspace is a device array inside the library of
+ * QIM_ATTENTION_NOALLOC_MAX_BYTES, one per device, held from the first call
+ * on a device until the process ends.  No reference counterpart: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops that forbid hipMalloc).  Arguments and output as qim_attention
+ * with v required (no V^T from a QKV GEMM); a problem whose
+ * qim_attention_workspace_bytes exceeds the maximum is rejected with
+ * QIM_ERR_SHAPE before anything is launched (S = T = 4352 with 24 heads fits
+ * for one batch).  Every call on a device shares its array: calls that
+ * overlap on one device race. */
+#define QIM_ATTENTION_NOALLOC_MAX_BYTES (64ll << 20)
+int qim_attention_noalloc(const void *q, int64_t ldq, const void *k, int64_t ldk, const void *v, int64_t ldv,
+                          void *o, int64_t ldo, int64_t B, int64_t S, int64_t T, int64_t H, int64_t D,
+                          float scale, void *stream);
+
 /* Test hooks: the device conversions every kernel uses, applied elementwise
  * (fp32 -> E4M3 code; fp32 -> bf16 bits), and one scaled MFMA
  * (32x32x64, E4M3 x E4M3) on a single tile: a (32, 64) codes, b (32, 64) codes

@@ -89,6 +89,11 @@ def test_abi_version():
                              None), _native.QIM_ERR_ARG),
     ("qim_attention_mxfp8", (16, 3072, 16, 3072, 16, 3072, 8, 16, 1, 16, 1 << 40, 1, 256, 256, 24, 128, 0.1,
                              None), _native.QIM_ERR_LAYOUT),
+    # attention without a workspace: v required; a problem above the scratch array (S = T = 16640, 24 heads)
+    ("qim_attention_noalloc", (16, 3072, 16, 3072, None, 3072, 16, 3072, 1, 256, 256, 24, 128, 0.1, None),
+     _native.QIM_ERR_ARG),
+    ("qim_attention_noalloc", (16, 3072, 16, 3072, 16, 3072, 16, 3072, 1, 16640, 16640, 24, 128, 0.1, None),
+     _native.QIM_ERR_SHAPE),
 ])
 def test_argument_checks_return_status(name, args, code):
     """Rejected before any launch: fake (aligned or misaligned) addresses are
