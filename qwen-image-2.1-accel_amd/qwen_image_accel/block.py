@@ -84,7 +84,8 @@ class MMDiTBlock:
         return MMDiTBlock.from_weights(w(3 * dim, dim), w(dim, dim), w(ffn, dim), w(ffn, dim),
                                        w(dim, ffn), nq, nk, heads)
 
-    def forward(self, h, modulation, freqs, attention_fn=None, attention_mxfp8_fn=None, fused_attention=False):
+    def forward(self, h, modulation, freqs, attention_fn=None, attention_mxfp8_fn=None, fused_attention=False,
+                stages=None):
         """h: (B, S, dim) bf16; modulation: (B, 6, dim) bf16 rows
         (shift1, scale1, gate1, shift2, scale2, gate2); freqs: (S, head_dim/2)
         complex64.  ``attention_fn(q, k, v) -> (B, S, dim)`` defaults to the
@@ -96,7 +97,9 @@ class MMDiTBlock:
         of its fusions: the QKV projection writes V straight into the
         attention's V^T tiles (S % 64 == 0) and the attention writes the
         out-projection's MXFP8 input -- the same bytes as
-        ``attention_fn=attention.attention``."""
+        ``attention_fn=attention.attention``.  ``stages``: a dict that
+        receives the intermediate results (x1, qkv, o, h1, x2, a) for
+        checking; nothing is copied."""
         b, s, d = h.shape
         shift1, scale1, _, shift2, scale2, _ = (modulation[:, i:i + 1] for i in range(6))
         gates = modulation[:, 2::3].tanh()                  # tanh(g1), tanh(g2) in one launch
@@ -130,6 +133,8 @@ class MMDiTBlock:
         x2 = layer_norm_scale_quantize(h1, scale2.contiguous(), norm, shift=shift2.contiguous(),
                                        add_one=True, tiled=True)
         a = self._mm(x2, self.w_gate_up, epilogue="swiglu_quant", out_tiled=True)
+        if stages is not None:
+            stages.update(x1=x, qkv=qkv, o=oq, h1=h1, x2=x2, a=a)
         h2 = self._mm(a, self.w_down, epilogue="gated_residual", gate=gate2.contiguous(),
                       residual=h1.reshape(b * s, d), seq=s)
         return h2.view(b, s, d)

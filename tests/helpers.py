@@ -66,3 +66,33 @@ def swizzle_permute(exponents):
 def bf16_randn(gen, shape, scale=1.0):
     """Seeded N(0, scale^2) bf16 tensor on the CPU."""
     return (torch.randn(shape, generator=gen) * scale).to(torch.bfloat16)
+
+
+def unswizzle_scales(flat, m, k):
+    """Flat swizzled E8M0 bytes of an (m, k) quantization -> (m, k/32)
+    exponents (the inverse of swizzle_permute; m % 128 == 0)."""
+    return np.asarray(flat, dtype=np.uint8).reshape(m // 128, k // 128, 32, 4, 4).transpose(0, 3, 2, 1, 4).reshape(
+        m, k // 32)
+
+
+def quantized_rows(q, rows):
+    """Codes (n, K) and exponents (n, K/32) of the given rows of a Quantized
+    (row-major or tiled) on any device, as numpy uint8."""
+    from qwen_image_accel.kernels import mxfp8
+    codes = mxfp8.as_row_major(q).values.view(torch.uint8)
+    mp, k = codes.shape
+    idx = torch.as_tensor(np.asarray(rows), device=codes.device)
+    exps = unswizzle_scales(q.scales.view(torch.uint8).cpu().numpy(), mp, k)
+    return codes[idx].cpu().numpy(), exps[np.asarray(rows)]
+
+
+def pack_quantized(codes, exps):
+    """Rows of codes (n, K) and exponents (n, K/32) -> an oracle-style
+    quantization of n rows: codes padded to a multiple of 128 rows with zeros
+    and the exponents swizzled."""
+    n, k = codes.shape
+    mp = (n + 127) // 128 * 128
+    q = np.zeros((mp, k), dtype=np.uint8)
+    e = np.zeros((mp, k // 32), dtype=np.uint8)
+    q[:n], e[:n] = codes, exps
+    return q, swizzle_permute(e)

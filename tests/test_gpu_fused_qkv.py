@@ -6,13 +6,16 @@ a head row inside one wave (whole tiles) or across two waves through LDS
 (quarter tiles of the partial last round: 612 tiles at M = 4352, H = 24), so
 these shapes cover both, plus padding rows (M = 4200) and two batches (seq <
 M, the RoPE row is row % seq).  The unfused path is held to the oracle by
-test_gpu_kernels.py.
+test_gpu_kernels.py, and the fused output directly to the oracle's norm +
+RoPE (oracle.norm_rope_pack) applied to the plain GEMM's bf16 Q/K columns.
 """
+import numpy as np
 import pytest
 import torch
 
+from oracle import oracle as O
 from qwen_image_accel.kernels import attention, gemm, mxfp8
-from tests.helpers import bf16_randn
+from tests.helpers import bf16_randn, bits
 
 pytestmark = pytest.mark.gpu
 
@@ -48,6 +51,13 @@ def test_qkv_gemm_with_qk_norm_rope_epilogue(dev, m, heads, k, seq):
         assert torch.equal(as16(fused[:, :d]), as16(oq.reshape(m, d))), "Q"
         assert torch.equal(as16(fused[:, d:2 * d]), as16(ok.reshape(m, d))), "K"
         assert torch.equal(as16(fused[:, 2 * d:]), as16(plain[:, 2 * d:])), "V"
+        # and the oracle's norm + RoPE of the plain GEMM's bf16 Q/K columns
+        pb = bits(plain).reshape(b, seq, 3, heads, 128)
+        rq, rk, _ = O.norm_rope_pack(pb[:, :, 0], pb[:, :, 1], pb[:, :, 0], bits(wq), bits(wk),
+                                     torch.view_as_real(freqs).cpu().numpy(), epsq=1e-6, epsk=1e-5)
+        fb = bits(fused).reshape(b, seq, 3, heads, 128)
+        assert np.array_equal(fb[:, :, 0], rq), "Q vs oracle"
+        assert np.array_equal(fb[:, :, 1], rk), "K vs oracle"
 
 
 def test_qkv_gemm_rejects_odd_heads(dev):

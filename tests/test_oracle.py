@@ -363,3 +363,23 @@ def test_bf16_round_helper_vs_torch():
 def test_golden_bits_roundtrip():
     x = torch.tensor([1.0, -2.5, 3e-39], dtype=torch.bfloat16)
     assert torch.equal(from_bits(bits(x)), x)
+
+
+def test_block_rows_subset_equals_full_block():
+    """oracle/block.py with rows= computes exactly those rows of the full
+    block (every step is row-local: the per-batch modulation, the RoPE row of
+    the token's position, the GEMM rows), across two batches."""
+    from oracle import block as OB
+    rng = np.random.default_rng(5)
+    B, S, D, H, F = 2, 150, 256, 2, 512
+    bf = lambda *shape, s=1.0: O.f32_to_bf16(rng.standard_normal(shape).astype(np.float32) * s)  # noqa: E731
+    w = {"qkv": bf(3 * D, D, s=0.05), "out": bf(D, D, s=0.05), "gate": bf(F, D, s=0.05), "up": bf(F, D, s=0.05),
+         "down": bf(D, F, s=0.05), "norm_q": O.f32_to_bf16(rng.uniform(0.8, 1.2, 128).astype(np.float32)),
+         "norm_k": O.f32_to_bf16(rng.uniform(0.8, 1.2, 128).astype(np.float32))}
+    h, mod = bf(B, S, D), bf(B, 6, D, s=0.3)
+    f = O.rope_freqs(O.rope_positions(6, 1, 12, 12))
+    full, st = OB.block_forward(h, mod, f, w, heads=H, return_stages=True)
+    rows = np.array([0, 7, 149, 150, 151, 299])
+    part = OB.block_forward(h, mod, f, w, heads=H, rows=rows)
+    assert np.array_equal(part, full.reshape(B * S, D)[rows])
+    assert np.isfinite(bf16_values(full)).all() and not np.array_equal(full, h)
