@@ -81,7 +81,7 @@ int qim_adaln(const void *x, const void *scale, const void *shift, const void *g
               float eps, int flags, void *stream);
 
 /* layer_norm_scale_quantize(x, scale, norm) -- src/qwen_image_accel/kernels/
- * epilogue.py:145-161 (kernel :92-142): qim_adaln's output quantized to MXFP8
+ * epilogue.py:76-92 (kernel :23-73): qim_adaln's output quantized to MXFP8
  * instead of stored.  q: (Mp, D), row-major or (QIM_ADALN_TILED) tiled;
  * scales: Mp*D/32.  D % 128 == 0. */
 int qim_adaln_quantize(const void *x, const void *scale, const void *shift, const void *gate,
@@ -102,7 +102,7 @@ int qim_swiglu(const void *g, int64_t ldg, const void *v, int64_t ldv, void *out
                int64_t M, int64_t F, void *stream);
 
 /* swiglu_quantize(gate, value) -- src/qwen_image_accel/kernels/epilogue.py:
- * 192-205 (kernel :164-189): swiglu quantized to MXFP8.  q: (Mp, F);
+ * 123-136 (kernel :95-120): swiglu quantized to MXFP8.  q: (Mp, F);
  * scales: Mp*F/32.  F % 128 == 0. */
 int qim_swiglu_quantize(const void *g, int64_t ldg, const void *v, int64_t ldv,
                         void *q, void *scales, int64_t M, int64_t F, void *stream);
@@ -148,7 +148,9 @@ int qim_qk_norm_rope_pack(const void *q, const void *k, const void *v, const voi
  * SWIGLU epilogues), or, for QIM_EPI_SWIGLU_QUANT, E4M3 codes (Mp, N/2) with
  * out_scales (Mp*N/64 bytes, swizzled).  bias: (N,) bf16.  gate: (B, N) bf16,
  * res: (M, N) bf16 (row stride N), B = ceil(M / seq).
- * K % 128 == 0, N % 256 == 0 (N % 512 == 0 for the SWIGLU epilogues). */
+ * K % 128 == 0, N % 128 == 0 (the reference converts a linear when K and N
+ * are multiples of 128, optimizations/mxfp8.py:15-16), N % 512 == 0 for the
+ * SWIGLU epilogues. */
 int qim_mxfp8_gemm(const void *aq, const void *as, const void *bq, const void *bs,
                    int64_t M, int64_t N, int64_t K, int epilogue, const void *bias,
                    const void *gate, const void *res, int64_t seq, void *out, int64_t ldo,
@@ -166,9 +168,15 @@ int qim_mxfp8_gemm(const void *aq, const void *as, const void *bq, const void *b
 #define QIM_GEMM_A_TILED 1   /* aq is tiled over Mp rows                          */
 #define QIM_GEMM_B_TILED 2   /* bq is tiled over N rows                           */
 #define QIM_GEMM_OUT_TILED 4 /* QIM_EPI_SWIGLU_QUANT codes are written tiled      */
+/* Output formats of QIM_EPI_NONE other than bf16 (torch._scaled_mm's out_dtype,
+ * optimizations/mxfp8.py:34-35): out is fp32 or fp16 (M, N), row stride ldo
+ * elements of that type. */
+#define QIM_GEMM_OUT_F32 8
+#define QIM_GEMM_OUT_F16 16
 
-/* qim_mxfp8_gemm with operand layouts (an OR of the flags above; 0 = both
- * row-major, which is qim_mxfp8_gemm itself). */
+/* qim_mxfp8_gemm with operand layouts and output format (an OR of the flags
+ * above; 0 = both operands row-major and a bf16 output, which is
+ * qim_mxfp8_gemm itself). */
 int qim_mxfp8_gemm_ex(const void *aq, const void *as, const void *bq, const void *bs,
                       int64_t M, int64_t N, int64_t K, int epilogue, int layouts,
                       const void *bias, const void *gate, const void *res, int64_t seq,

@@ -107,7 +107,7 @@ __global__ __launch_bounds__(256) void k_attn_vt(const uint16_t *__restrict__ v,
 
 // ------------------------------------------------------------- forward --
 __device__ __forceinline__ void att_dma16(const void *base, uint32_t voff, uint32_t lds_addr) {
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds_addr)
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "{m0}"(lds_addr)
                  : "memory");
 }
 __device__ __forceinline__ uint32_t att_lds_addr(const void *p) {
@@ -722,7 +722,7 @@ int attention_run(const char *who, const void *q, int64_t ldq, const void *k, in
     hipStream_t st = as_stream(stream);
     uint8_t *ws = static_cast<uint8_t *>(workspace);
     if (v)
-        hipLaunchKernelGGL(k_attn_vt, dim3((unsigned)nkb, (unsigned)H, (unsigned)B), dim3(256), 0, st,
+        launch(k_attn_vt, dim3((unsigned)nkb, (unsigned)H, (unsigned)B), dim3(256), 0, st,
                            (const uint16_t *)v, ldv, (uint16_t *)ws, (int)T, (int)H, (int)nkb);
     AttnArgs a{};
     a.q = (const uint16_t *)q;
@@ -751,16 +751,16 @@ int attention_run(const char *who, const void *q, int64_t ldq, const void *k, in
     a.tiled = tiled;
     const int64_t nwg = pl.nfull + pl.ntail * pl.nsplit;
     if (qcodes)
-        hipLaunchKernelGGL(k_attn_fwd<true>, dim3((unsigned)nwg), dim3(256), ATT_LDS, st, a);
+        launch(k_attn_fwd<true>, dim3((unsigned)nwg), dim3(256), ATT_LDS, st, a);
     else
-        hipLaunchKernelGGL(k_attn_fwd<false>, dim3((unsigned)nwg), dim3(256), ATT_LDS, st, a);
+        launch(k_attn_fwd<false>, dim3((unsigned)nwg), dim3(256), ATT_LDS, st, a);
     if (pl.ntail) {
         const int64_t threads = pl.ntail * ATT_BQ * (ATT_D / 8);
-        hipLaunchKernelGGL(k_attn_merge, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, a);
+        launch(k_attn_merge, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, a);
     }
     if (qcodes && a.Mp > M) {
         const int64_t threads = (a.Mp - M) * H * ATT_D / 16;
-        hipLaunchKernelGGL(k_attn_qpad, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, a, M);
+        launch(k_attn_qpad, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, a, M);
     }
     return check_launch(who);
 }

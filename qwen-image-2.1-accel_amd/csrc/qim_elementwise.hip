@@ -63,7 +63,7 @@ extern "C" int qim_gated_residual(const void *h, const void *x, const void *gate
     QIM_REQUIRE(aligned16(h) && aligned16(x) && aligned16(gate) && aligned16(out), QIM_ERR_LAYOUT,
                 "qim_gated_residual: operands must be 16-byte aligned");
     const uint32_t nvec = (uint32_t)(rows * D / 8);
-    hipLaunchKernelGGL(k_gated_residual, dim3((nvec + 255) / 256), dim3(256), 0, as_stream(stream),
+    launch(k_gated_residual, dim3((nvec + 255) / 256), dim3(256), 0, as_stream(stream),
                        (const uint16_t *)h, (const uint16_t *)x, (const uint16_t *)gate, (uint16_t *)out, nvec,
                        (uint32_t)(D / 8), (uint32_t)(seq * D / 8));
     return check_launch("qim_gated_residual");
@@ -82,7 +82,7 @@ extern "C" int qim_swiglu(const void *g, int64_t ldg, const void *v, int64_t ldv
     // grid.y is limited to 65535: fold extra rows into repeated launches.
     for (int64_t r0 = 0; r0 < M; r0 += 65535) {
         const int64_t n = M - r0 < 65535 ? M - r0 : 65535;
-        hipLaunchKernelGGL(k_swiglu, dim3((f8 + 255) / 256, (unsigned)n), dim3(256), 0, as_stream(stream),
+        launch(k_swiglu, dim3((f8 + 255) / 256, (unsigned)n), dim3(256), 0, as_stream(stream),
                            (const uint16_t *)g + r0 * ldg, ldg, (const uint16_t *)v + r0 * ldv, ldv,
                            (uint16_t *)out + r0 * ldo, ldo, f8);
         int rc = check_launch("qim_swiglu");

@@ -52,8 +52,10 @@ struct GemmArgs {
     void *out;
     int64_t ldo;
     uint8_t *out_scales;
-    int tiles_m, tiles_n;
+    int tiles_m, tiles_n;  // 256 x 256 tiles (tiles_n: whole 256-column blocks)
     int main_tiles;  // whole tiles; workgroups past them compute quarter tiles of the rest
+    int quarters;    // quarter tiles of whole tiles; the ones after them cover a last
+                     // 128-column block (N % 256 == 128), 128 rows each
     int a_tiled, b_tiled, out_tiled;  // code layouts (mxt_offset) of A, B and a quantized output
     // QIM_EPI_QK_NORM_ROPE: head weights, RoPE table (seq rows of 128 fp32),
     // and the column ends of Q (H * 128) and K (2 * H * 128).
@@ -77,6 +79,9 @@ struct GemmArgs {
 constexpr int EPI_QKV_VT = 6;
 template <int EPI>
 constexpr bool is_qk_epi() { return EPI == QIM_EPI_QK_NORM_ROPE || EPI == EPI_QKV_VT; }
+// QIM_EPI_NONE with an fp32 or fp16 output (QIM_GEMM_OUT_F32 / _F16): the
+// reference's out_dtype of torch._scaled_mm.
+constexpr int EPI_F32 = 7, EPI_F16 = 8;
 
 template <typename V>
 __device__ __forceinline__ void st_out(bool cached, void *ptr, const V &v) {
@@ -167,15 +172,17 @@ __device__ __forceinline__ LoadPlan make_plan(const GemmArgs &p, int64_t m0, int
 // so it does not force vmcnt(0) before every LDS read (it cannot prove the
 // ring slots disjoint); the ring's own vmcnt waits and s_barrier order them.
 // M0 holds the wave-uniform LDS destination; lane i lands at M0 + 16i (4i for
-// the dword form).  M0 is set inside the statement, right before its use.
+// the dword form).  The destination is an "{m0}" operand, so the compiler
+// writes M0 itself and knows its value at every statement; the s_nop covers
+// the wait state between that write and the DMA's read of M0.
 __device__ __forceinline__ void dma16(const uint8_t *base, uint32_t voff, uint32_t lds_addr) {
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base),
-                 "s"(lds_addr)
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base),
+                 "{m0}"(lds_addr)
                  : "memory");
 }
 __device__ __forceinline__ void dma4(const uint8_t *base, uint32_t voff, uint32_t lds_addr) {
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(base),
-                 "s"(lds_addr)
+    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(base),
+                 "{m0}"(lds_addr)
                  : "memory");
 }
 
@@ -358,6 +365,27 @@ __device__ __forceinline__ int epi_col_offset(int c) { return c * 8 + (c >> 3) *
 template <int EPI, int TI, int TJ>
 __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][TJ], uint8_t *lds, int64_t row0,
                                          int64_t gcol0, int lane, int wave) {
+    if constexpr (EPI == EPI_F32 || EPI == EPI_F16) {
+        // Straight from the accumulators: for each register, 32 lanes store
+        // 32 consecutive columns of one row (128 or 64 contiguous bytes).
+        const int lr = lane & 31, kh = lane >> 5;
+#pragma unroll
+        for (int ti = 0; ti < TI; ++ti)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int64_t row = row0 + 32 * ti + 8 * (i / 4) + 4 * kh + (i % 4);
+                if (row >= p.M) continue;
+#pragma unroll
+                for (int tj = 0; tj < TJ; ++tj) {
+                    const int64_t o = row * p.ldo + gcol0 + 32 * tj + lr;
+                    if constexpr (EPI == EPI_F32)
+                        __builtin_nontemporal_store(acc[ti][tj][i], reinterpret_cast<float *>(p.out) + o);
+                    else
+                        __builtin_nontemporal_store((_Float16)acc[ti][tj][i], reinterpret_cast<_Float16 *>(p.out) + o);
+                }
+            }
+        return;
+    } else {
     constexpr bool SWI = EPI == QIM_EPI_SWIGLU || EPI == QIM_EPI_SWIGLU_QUANT;
     constexpr int W = SWI ? 16 * TJ : 32 * TJ;  // output columns of this wave
     constexpr int RGS = W * 8 + (W / 8) * 16;   // bytes per group of 4 rows
@@ -566,6 +594,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
             }
         }
     }
+    }
 }
 
 // ------------------------------------------------------------ tail tiles --
@@ -675,10 +704,17 @@ __device__ __forceinline__ void qstep(const GemmArgs &p, const QPlan &Q, uint8_t
 
 template <int EPI>
 __device__ __forceinline__ void quarter_tile(const GemmArgs &p, uint8_t *lds, int q) {
-    const int tile = p.main_tiles + q / 4, quarter = q & 3;
-    int tm, tn;
-    tile_coords(p, tile, tm, tn);
-    const int64_t m0 = (int64_t)tm * BM + (quarter >> 1) * 128, n0 = (int64_t)tn * BN + (quarter & 1) * 128;
+    int64_t m0, n0;
+    if (q < p.quarters) {  // a quarter of one of the last whole tiles
+        const int tile = p.main_tiles + q / 4, quarter = q & 3;
+        int tm, tn;
+        tile_coords(p, tile, tm, tn);
+        m0 = (int64_t)tm * BM + (quarter >> 1) * 128;
+        n0 = (int64_t)tn * BN + (quarter & 1) * 128;
+    } else {               // 128 rows of the last 128-column block
+        m0 = (int64_t)(q - p.quarters) * 128;
+        n0 = (int64_t)p.tiles_n * BN;
+    }
     if (m0 >= p.Mp) return;  // padding rows only (whole workgroup)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1, lr = lane & 31, kh = lane >> 5;
@@ -760,13 +796,14 @@ static int64_t main_tile_count(int64_t tiles) {
 }
 
 template <int EPI>
-static int launch_gemm(const GemmArgs &a, int64_t tiles, hipStream_t st) {
+static int launch_gemm(const GemmArgs &a, hipStream_t st) {
     static bool configured[QIM_MAX_DEVICES] = {};
     if (const int rc = reserve_lds(reinterpret_cast<const void *>(&k_mx_gemm<EPI>), LDS_BYTES, configured,
                                    "qim_mxfp8_gemm"))
         return rc;
-    const int64_t grid = a.main_tiles + 4 * (tiles - a.main_tiles);
-    hipLaunchKernelGGL(k_mx_gemm<EPI>, dim3((unsigned)grid), dim3(256), LDS_BYTES, st, a);
+    const int64_t half_column = a.tiles_n * BN < a.N ? (a.Mp + 127) / 128 : 0;
+    const int64_t grid = a.main_tiles + a.quarters + half_column;
+    launch(k_mx_gemm<EPI>, dim3((unsigned)grid), dim3(256), LDS_BYTES, st, a);
     return QIM_OK;
 }
 
@@ -786,13 +823,18 @@ static int gemm_run(const void *aq, const void *as, const void *bq, const void *
                     int epilogue, int layouts, const void *bias, const void *gate, const void *res, int64_t seq,
                     void *out, int64_t ldo, void *out_scales, const QKNormRope *qk, void *stream) {
     QIM_REQUIRE(aq && as && bq && bs && out, QIM_ERR_ARG, "qim_mxfp8_gemm: null pointer");
-    QIM_REQUIRE((layouts & ~(QIM_GEMM_A_TILED | QIM_GEMM_B_TILED | QIM_GEMM_OUT_TILED)) == 0, QIM_ERR_ARG,
-                "qim_mxfp8_gemm: unknown layout flags 0x%x", layouts);
+    constexpr int KNOWN = QIM_GEMM_A_TILED | QIM_GEMM_B_TILED | QIM_GEMM_OUT_TILED | QIM_GEMM_OUT_F32 | QIM_GEMM_OUT_F16;
+    QIM_REQUIRE((layouts & ~KNOWN) == 0, QIM_ERR_ARG, "qim_mxfp8_gemm: unknown layout flags 0x%x", layouts);
+    const int out_format = layouts & (QIM_GEMM_OUT_F32 | QIM_GEMM_OUT_F16);
+    QIM_REQUIRE(out_format != (QIM_GEMM_OUT_F32 | QIM_GEMM_OUT_F16), QIM_ERR_ARG,
+                "qim_mxfp8_gemm: QIM_GEMM_OUT_F32 and QIM_GEMM_OUT_F16 exclude each other");
+    QIM_REQUIRE(!out_format || epilogue == QIM_EPI_NONE, QIM_ERR_ARG,
+                "qim_mxfp8_gemm: an fp32 / fp16 output is available with QIM_EPI_NONE only");
     QIM_REQUIRE(!(layouts & QIM_GEMM_OUT_TILED) || epilogue == QIM_EPI_SWIGLU_QUANT, QIM_ERR_ARG,
                 "qim_mxfp8_gemm: a tiled output needs the quantized SwiGLU epilogue");
     QIM_REQUIRE(M > 0 && N > 0 && K > 0, QIM_ERR_SHAPE, "qim_mxfp8_gemm: empty problem");
     QIM_REQUIRE(K % 128 == 0, QIM_ERR_SHAPE, "qim_mxfp8_gemm: K=%lld is not a multiple of 128", (long long)K);
-    QIM_REQUIRE(N % BN == 0, QIM_ERR_SHAPE, "qim_mxfp8_gemm: N=%lld is not a multiple of 256", (long long)N);
+    QIM_REQUIRE(N % 128 == 0, QIM_ERR_SHAPE, "qim_mxfp8_gemm: N=%lld is not a multiple of 128", (long long)N);
     const int64_t Mp = (M + 127) / 128 * 128;
     const int64_t tiles_m = (Mp + BM - 1) / BM, tiles_n = N / BN;
     QIM_REQUIRE(4 * tiles_m * tiles_n < (1ll << 31), QIM_ERR_SHAPE, "qim_mxfp8_gemm: too many tiles");
@@ -801,11 +843,12 @@ static int gemm_run(const void *aq, const void *as, const void *bq, const void *
                 QIM_ERR_LAYOUT, "qim_mxfp8_gemm: operands must be 16-byte aligned");
     QIM_REQUIRE(epilogue == QIM_EPI_SWIGLU_QUANT || ldo % 8 == 0, QIM_ERR_LAYOUT,
                 "qim_mxfp8_gemm: ldo=%lld is not a multiple of 8", (long long)ldo);
+    QIM_REQUIRE(Mp / 128 < (1ll << 30), QIM_ERR_SHAPE, "qim_mxfp8_gemm: M=%lld too large", (long long)M);
     QIM_REQUIRE(Mp * K < (1ll << 31) && N * K < (1ll << 31), QIM_ERR_SHAPE,
                 "qim_mxfp8_gemm: operands above 2 GiB are not supported");
     GemmArgs a{(const uint8_t *)aq, (const uint8_t *)as, (const uint8_t *)bq, (const uint8_t *)bs, M, Mp, N, K,
                (const uint16_t *)bias, (const uint16_t *)gate, (const uint16_t *)res, seq > 0 ? seq : M, out, ldo,
-               (uint8_t *)out_scales, (int)tiles_m, (int)tiles_n, 0,
+               (uint8_t *)out_scales, (int)tiles_m, (int)tiles_n, 0, 0,
                (layouts & QIM_GEMM_A_TILED) != 0, (layouts & QIM_GEMM_B_TILED) != 0,
                (layouts & QIM_GEMM_OUT_TILED) != 0,
                nullptr, nullptr, nullptr, 0.0f, 0.0f, 0, 0, nullptr, 0};
@@ -822,37 +865,43 @@ static int gemm_run(const void *aq, const void *as, const void *bq, const void *
     }
     const int64_t tiles = tiles_m * tiles_n;
     a.main_tiles = (int)main_tile_count(tiles);
+    a.quarters = (int)(4 * (tiles - a.main_tiles));
     int rc;
     switch (epilogue) {
         case QIM_EPI_NONE:
             QIM_REQUIRE(ldo >= N, QIM_ERR_LAYOUT, "qim_mxfp8_gemm: ldo=%lld < N", (long long)ldo);
-            rc = launch_gemm<QIM_EPI_NONE>(a, tiles, as_stream(stream));
+            if (out_format == QIM_GEMM_OUT_F32)
+                rc = launch_gemm<EPI_F32>(a, as_stream(stream));
+            else if (out_format == QIM_GEMM_OUT_F16)
+                rc = launch_gemm<EPI_F16>(a, as_stream(stream));
+            else
+                rc = launch_gemm<QIM_EPI_NONE>(a, as_stream(stream));
             break;
         case QIM_EPI_BIAS:
             QIM_REQUIRE(bias, QIM_ERR_ARG, "qim_mxfp8_gemm: bias epilogue without bias");
             QIM_REQUIRE(ldo >= N, QIM_ERR_LAYOUT, "qim_mxfp8_gemm: ldo=%lld < N", (long long)ldo);
-            rc = launch_gemm<QIM_EPI_BIAS>(a, tiles, as_stream(stream));
+            rc = launch_gemm<QIM_EPI_BIAS>(a, as_stream(stream));
             break;
         case QIM_EPI_GATED_RESIDUAL:
             QIM_REQUIRE(gate && res, QIM_ERR_ARG, "qim_mxfp8_gemm: gated residual needs gate and res");
             QIM_REQUIRE(ldo >= N, QIM_ERR_LAYOUT, "qim_mxfp8_gemm: ldo=%lld < N", (long long)ldo);
-            rc = launch_gemm<QIM_EPI_GATED_RESIDUAL>(a, tiles, as_stream(stream));
+            rc = launch_gemm<QIM_EPI_GATED_RESIDUAL>(a, as_stream(stream));
             break;
         case QIM_EPI_SWIGLU:
             QIM_REQUIRE(N % 512 == 0, QIM_ERR_SHAPE, "qim_mxfp8_gemm: SwiGLU needs N %% 512 == 0");
             QIM_REQUIRE(ldo >= N / 2, QIM_ERR_LAYOUT, "qim_mxfp8_gemm: ldo=%lld < N/2", (long long)ldo);
-            rc = launch_gemm<QIM_EPI_SWIGLU>(a, tiles, as_stream(stream));
+            rc = launch_gemm<QIM_EPI_SWIGLU>(a, as_stream(stream));
             break;
         case QIM_EPI_SWIGLU_QUANT:
             QIM_REQUIRE(N % 512 == 0, QIM_ERR_SHAPE, "qim_mxfp8_gemm: SwiGLU needs N %% 512 == 0");
             QIM_REQUIRE(out_scales, QIM_ERR_ARG, "qim_mxfp8_gemm: quantized output needs out_scales");
-            rc = launch_gemm<QIM_EPI_SWIGLU_QUANT>(a, tiles, as_stream(stream));
+            rc = launch_gemm<QIM_EPI_SWIGLU_QUANT>(a, as_stream(stream));
             break;
         case QIM_EPI_QK_NORM_ROPE:
             QIM_REQUIRE(qk, QIM_ERR_ARG, "qim_mxfp8_gemm: the QK epilogue is qim_mxfp8_gemm_qk_norm_rope's");
             QIM_REQUIRE(ldo >= N, QIM_ERR_LAYOUT, "qim_mxfp8_gemm: ldo=%lld < N", (long long)ldo);
-            rc = qk->vt ? launch_gemm<EPI_QKV_VT>(a, tiles, as_stream(stream))
-                        : launch_gemm<QIM_EPI_QK_NORM_ROPE>(a, tiles, as_stream(stream));
+            rc = qk->vt ? launch_gemm<EPI_QKV_VT>(a, as_stream(stream))
+                        : launch_gemm<QIM_EPI_QK_NORM_ROPE>(a, as_stream(stream));
             break;
         default:
             return fail(QIM_ERR_ARG, "qim_mxfp8_gemm: unknown epilogue %d", epilogue);

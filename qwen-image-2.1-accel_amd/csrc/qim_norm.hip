@@ -44,7 +44,7 @@ constexpr uint32_t BF16X2_NEG_ZERO = 0x80008000u, BF16X2_ONE = 0x3f803f80u;
 // One modulated LayerNorm row per workgroup of W waves (reference chain, eager
 // rounding points: t0 = bf16(LN x), t1 = scale or bf16(1 + scale),
 // t2 = bf16(t1 t0), t3 = bf16(t2 + shift), t4 = bf16(gate t3),
-// out = bf16(res + t4); kernels/layernorm.py:49-55, kernels/epilogue.py:127-133).
+// out = bf16(res + t4); kernels/layernorm.py:49-55, kernels/epilogue.py:56-63).
 // Thread t holds the 16-byte vectors t, t + 64 W, ... (NV of them) of the row;
 // the two-pass float64 statistics are reduced inside each wave, then across
 // the W waves through LDS.  Every load is issued before the first reduction.
@@ -257,29 +257,29 @@ static int launch_adaln_rg(const AdaLNArgs &a, hipStream_t st) {
         // quantizing 15.3 vs 17.0 us (4352 rows), bf16 with residual and gate
         // 7.92 vs 7.76 us (1280 rows).
         if (!QUANT && k % 2 == 0 && k / 2 <= ADALN_FULL_WAVES) {
-            hipLaunchKernelGGL((k_adaln<QUANT, 2, true, RG>), grid, dim3(64 * (k / 2)), 0, st, a);
+            launch((k_adaln<QUANT, 2, true, RG>), grid, dim3(64 * (k / 2)), 0, st, a);
             return QIM_OK;
         }
         if (k % 3 == 0 && k / 3 <= ADALN_FULL_WAVES) {
-            hipLaunchKernelGGL((k_adaln<QUANT, 3, true, RG>), grid, dim3(64 * (k / 3)), 0, st, a);
+            launch((k_adaln<QUANT, 3, true, RG>), grid, dim3(64 * (k / 3)), 0, st, a);
             return QIM_OK;
         }
         if (k % 4 == 0 && k / 4 <= ADALN_FULL_WAVES) {
-            hipLaunchKernelGGL((k_adaln<QUANT, 4, true, RG>), grid, dim3(64 * (k / 4)), 0, st, a);
+            launch((k_adaln<QUANT, 4, true, RG>), grid, dim3(64 * (k / 4)), 0, st, a);
             return QIM_OK;
         }
         if (k % 2 == 0 && k / 2 <= ADALN_FULL_WAVES) {
-            hipLaunchKernelGGL((k_adaln<QUANT, 2, true, RG>), grid, dim3(64 * (k / 2)), 0, st, a);
+            launch((k_adaln<QUANT, 2, true, RG>), grid, dim3(64 * (k / 2)), 0, st, a);
             return QIM_OK;
         }
         if (k <= ADALN_FULL_WAVES) {
-            hipLaunchKernelGGL((k_adaln<QUANT, 1, true, RG>), grid, dim3(64 * k), 0, st, a);
+            launch((k_adaln<QUANT, 1, true, RG>), grid, dim3(64 * k), 0, st, a);
             return QIM_OK;
         }
     }
     const int waves = (nvec + 127) / 128;
     if (waves > ADALN_MAX_WAVES) return fail(QIM_ERR_SHAPE, "adaln: D=%d exceeds %d", a.D, 8 * 128 * ADALN_MAX_WAVES);
-    hipLaunchKernelGGL((k_adaln<QUANT, 2, false, RG>), grid, dim3(64 * waves), 0, st, a);
+    launch((k_adaln<QUANT, 2, false, RG>), grid, dim3(64 * waves), 0, st, a);
     return QIM_OK;
 }
 
@@ -412,7 +412,7 @@ static void launch_norm_rope_shape(NormRopeArgs a, int64_t prefix_blocks, hipStr
     a.groups = (uint32_t)groups;
     a.main_waves = (uint32_t)waves;
     a.main_blocks = (waves + 3) / 4;
-    hipLaunchKernelGGL((k_norm_rope<D, NORM, ROPE, NTENS, U, FULL>), dim3((unsigned)(a.main_blocks + prefix_blocks)),
+    launch((k_norm_rope<D, NORM, ROPE, NTENS, U, FULL>), dim3((unsigned)(a.main_blocks + prefix_blocks)),
                        dim3(256), 0, st, a);
 }
 

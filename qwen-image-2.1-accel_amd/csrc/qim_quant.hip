@@ -30,7 +30,7 @@ struct QuantSource {
 };
 
 // SwiGLU source: swiglu_quantize(g, v) (reference kernels/epilogue.py:
-// 164-189): the bf16 value of bf16(silu(g)) * v, exactly what the unfused
+// 95-120): the bf16 value of bf16(silu(g)) * v, exactly what the unfused
 // path stores before quantizing.
 struct SwigluSource {
     const uint16_t *g;
@@ -107,7 +107,7 @@ static int mx_quantize(const void *x, int64_t ldx, int64_t M, int64_t K, void *q
                 "qim_mx_quantize: x must be 16-byte aligned with ldx %% 8 == 0 (ldx=%lld)", (long long)ldx);
     dim3 grid((unsigned)((M + 127) / 128), (unsigned)(K / 128));
     QuantSource src{(const uint16_t *)x, ldx};
-    hipLaunchKernelGGL(k_quant_tile<QuantSource>, grid, dim3(256), 0, as_stream(stream), src, (uint8_t *)q,
+    launch(k_quant_tile<QuantSource>, grid, dim3(256), 0, as_stream(stream), src, (uint8_t *)q,
                        (uint8_t *)scales, M, K, tiled);
     return check_launch("qim_mx_quantize");
 }
@@ -122,7 +122,7 @@ static int swiglu_quantize(const void *g, int64_t ldg, const void *v, int64_t ld
                 QIM_ERR_LAYOUT, "qim_swiglu_quantize: inputs must be 16-byte aligned with strides %% 8 == 0");
     dim3 grid((unsigned)((M + 127) / 128), (unsigned)(F / 128));
     SwigluSource src{(const uint16_t *)g, ldg, (const uint16_t *)v, ldv};
-    hipLaunchKernelGGL(k_quant_tile<SwigluSource>, grid, dim3(256), 0, as_stream(stream), src, (uint8_t *)q,
+    launch(k_quant_tile<SwigluSource>, grid, dim3(256), 0, as_stream(stream), src, (uint8_t *)q,
                        (uint8_t *)scales, M, F, tiled);
     return check_launch("qim_swiglu_quantize");
 }

@@ -17,9 +17,18 @@ int fail(int code, const char *fmt, ...) {
     return code;
 }
 
+hipError_t &launch_error() {
+    static thread_local hipError_t e = hipSuccess;
+    return e;
+}
+
 int check_launch(const char *what) {
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return fail(QIM_ERR_LAUNCH, "%s: launch failed: %s", what, hipGetErrorString(e));
+    const hipError_t e = launch_error();
+    launch_error() = hipSuccess;
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(QIM_ERR_LAUNCH, "%s: launch failed: %s", what, hipGetErrorString(e));
+    }
     g_error[0] = '\0';
     return QIM_OK;
 }
@@ -168,7 +177,7 @@ extern "C" int qim_debug_silu(const void *g, void *out, int64_t n, void *stream)
     QIM_REQUIRE(g && out && n >= 0, QIM_ERR_ARG, "qim_debug_silu: bad arguments");
     QIM_REQUIRE((n + 255) / 256 < (1ll << 31), QIM_ERR_SHAPE, "qim_debug_silu: too large");
     if (n == 0) return QIM_OK;
-    hipLaunchKernelGGL(k_debug_silu, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, as_stream(stream),
+    launch(k_debug_silu, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, as_stream(stream),
                        (const uint16_t *)g, (uint16_t *)out, n);
     return check_launch("qim_debug_silu");
 }
@@ -180,7 +189,7 @@ extern "C" int qim_debug_copy(const void *src, void *dst, int64_t nbytes, void *
     const int64_t nvec = nbytes / 16;
     QIM_REQUIRE((nvec + 255) / 256 < (1ll << 31), QIM_ERR_SHAPE, "qim_debug_copy: too large");
     if (nvec == 0) return QIM_OK;
-    hipLaunchKernelGGL(k_debug_copy, dim3((unsigned)((nvec + 255) / 256)), dim3(256), 0, as_stream(stream),
+    launch(k_debug_copy, dim3((unsigned)((nvec + 255) / 256)), dim3(256), 0, as_stream(stream),
                        (const uint4 *)src, (uint4 *)dst, nvec);
     return check_launch("qim_debug_copy");
 }
@@ -188,9 +197,9 @@ extern "C" int qim_debug_copy(const void *src, void *dst, int64_t nbytes, void *
 extern "C" int qim_debug_mfma_probe(int shape, float *out, void *stream) {
     QIM_REQUIRE(out && (shape == 0 || shape == 1), QIM_ERR_ARG, "qim_debug_mfma_probe: bad arguments");
     if (shape == 0)
-        hipLaunchKernelGGL(k_debug_mfma_probe<0>, dim3(4096), dim3(64), 0, as_stream(stream), out);
+        launch(k_debug_mfma_probe<0>, dim3(4096), dim3(64), 0, as_stream(stream), out);
     else
-        hipLaunchKernelGGL(k_debug_mfma_probe<1>, dim3(4096), dim3(64), 0, as_stream(stream), out);
+        launch(k_debug_mfma_probe<1>, dim3(4096), dim3(64), 0, as_stream(stream), out);
     return check_launch("qim_debug_mfma_probe");
 }
 
@@ -202,7 +211,7 @@ extern "C" int qim_debug_e4m3_encode(const float *x, void *codes, int64_t n, voi
     QIM_REQUIRE(x && codes && n >= 0, QIM_ERR_ARG, "qim_debug_e4m3_encode: bad arguments");
     if (n == 0) return QIM_OK;
     int64_t threads = (n + 3) / 4;
-    hipLaunchKernelGGL(k_debug_e4m3, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+    launch(k_debug_e4m3, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
                        as_stream(stream), x, (uint8_t *)codes, n);
     return check_launch("qim_debug_e4m3_encode");
 }
@@ -210,7 +219,7 @@ extern "C" int qim_debug_e4m3_encode(const float *x, void *codes, int64_t n, voi
 extern "C" int qim_debug_bf16_round(const float *x, void *bits, int64_t n, void *stream) {
     QIM_REQUIRE(x && bits && n >= 0, QIM_ERR_ARG, "qim_debug_bf16_round: bad arguments");
     if (n == 0) return QIM_OK;
-    hipLaunchKernelGGL(k_debug_bf16, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+    launch(k_debug_bf16, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
                        as_stream(stream), x, (uint16_t *)bits, n);
     return check_launch("qim_debug_bf16_round");
 }
@@ -219,7 +228,7 @@ extern "C" int qim_debug_mfma_tile(const void *a, const void *b, const void *sa,
                                    float *out, void *stream) {
     QIM_REQUIRE(a && b && sa && sb && out, QIM_ERR_ARG, "qim_debug_mfma_tile: null pointer");
     QIM_REQUIRE(aligned16(a) && aligned16(b), QIM_ERR_LAYOUT, "qim_debug_mfma_tile: a, b must be 16-byte aligned");
-    hipLaunchKernelGGL(k_debug_mfma, dim3(1), dim3(64), 0, as_stream(stream), (const uint8_t *)a,
+    launch(k_debug_mfma, dim3(1), dim3(64), 0, as_stream(stream), (const uint8_t *)a,
                        (const uint8_t *)b, (const uint8_t *)sa, (const uint8_t *)sb, out);
     return check_launch("qim_debug_mfma_tile");
 }

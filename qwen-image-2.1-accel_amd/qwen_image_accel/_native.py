@@ -16,7 +16,7 @@ LIB_PATH = os.environ.get("QIM_LIBRARY", os.path.join(os.path.dirname(os.path.ab
 
 QIM_OK, QIM_ERR_ARG, QIM_ERR_SHAPE, QIM_ERR_LAYOUT, QIM_ERR_LAUNCH = range(5)
 ADALN_ADD_ONE, ADALN_TILED = 1, 2
-GEMM_A_TILED, GEMM_B_TILED, GEMM_OUT_TILED = 1, 2, 4
+GEMM_A_TILED, GEMM_B_TILED, GEMM_OUT_TILED, GEMM_OUT_F32, GEMM_OUT_F16 = 1, 2, 4, 8, 16
 EPI_NONE, EPI_BIAS, EPI_GATED_RESIDUAL, EPI_SWIGLU, EPI_SWIGLU_QUANT, EPI_QK_NORM_ROPE = range(6)
 SWIGLU_GROUP = 32
 

@@ -1,8 +1,8 @@
 """Fused MXFP8 producers: FP8 straight out of the LayerNorm and the SwiGLU.
 
 Reference interface: src/qwen_image_accel/kernels/epilogue.py
-``layer_norm_scale_quantize(x, scale, norm)`` (:145-161) and
-``swiglu_quantize(gate, value)`` (:192-205).  Each returns a ``Quantized``
+``layer_norm_scale_quantize(x, scale, norm)`` (:76-92, kernel :23-73) and
+``swiglu_quantize(gate, value)`` (:123-136, kernel :95-120).  Each returns a ``Quantized``
 byte-identical to ``quantize`` of the unfused bf16 result, or ``None`` when the
 inputs are unsupported (the caller then takes the unfused path,
 optimizations/quantized_decode.py:99-105).  ``tiled=True`` (no reference

@@ -84,8 +84,11 @@ def interleave_swiglu(gate_weight, up_weight, group=_native.SWIGLU_GROUP):
                         up_weight.reshape(f // group, group, k)], dim=1).reshape(2 * f, k)
 
 
+_OUT_FORMATS = {torch.bfloat16: 0, torch.float32: _native.GEMM_OUT_F32, torch.float16: _native.GEMM_OUT_F16}
+
+
 def mx_matmul(activation, weight_fp8, weight_scale, *, epilogue="none", bias=None, gate=None,
-              residual=None, seq=None, out=None, weight_tiled=False, out_tiled=False):
+              residual=None, seq=None, out=None, weight_tiled=False, out_tiled=False, dtype=torch.bfloat16):
     """``activation @ weight.T`` in MXFP8 with a fused epilogue.
 
     activation: ``Quantized`` (Mp, K), row-major or tiled (``TiledQuantized``).
@@ -94,8 +97,15 @@ def mx_matmul(activation, weight_fp8, weight_scale, *, epilogue="none", bias=Non
     weight_scale: its swizzled scales.  Returns bf16 (rows, N) -- (rows, N/2)
     for "swiglu" -- or a ``Quantized`` (rows, N/2) for "swiglu_quant"
     (``TiledQuantized`` with ``out_tiled=True``).  ``gate`` is (B, 1, N) or
-    (B, N) with ``seq`` rows per batch; ``residual`` is (rows, N)."""
+    (B, N) with ``seq`` rows per batch; ``residual`` is (rows, N).  ``dtype``:
+    the output type of the plain epilogue ("none"): bf16, fp32 or fp16, as
+    torch._scaled_mm's out_dtype (optimizations/mxfp8.py:34-35); the other
+    epilogues write bf16."""
     epi = EPILOGUES[epilogue]
+    if dtype not in _OUT_FORMATS:
+        raise ValueError(f"the MXFP8 GEMM writes bf16, fp32 or fp16, not {dtype}")
+    if dtype != torch.bfloat16 and epi != _native.EPI_NONE:
+        raise ValueError(f"a {dtype} output is available with the plain epilogue only")
     a = activation
     w = weight_fp8 if weight_tiled else weight_rows(weight_fp8)
     if weight_tiled and not w.is_contiguous():
@@ -104,7 +114,7 @@ def mx_matmul(activation, weight_fp8, weight_scale, *, epilogue="none", bias=Non
     if out_tiled and epi != _native.EPI_SWIGLU_QUANT:
         raise ValueError("out_tiled applies to the quantized SwiGLU epilogue only")
     layouts = ((_native.GEMM_A_TILED if a.tiled else 0) | (_native.GEMM_B_TILED if weight_tiled else 0)
-               | (_native.GEMM_OUT_TILED if out_tiled else 0))
+               | (_native.GEMM_OUT_TILED if out_tiled else 0) | _OUT_FORMATS[dtype])
     if a.values.shape[1] != k:
         raise ValueError(f"activation K={a.values.shape[1]} does not match weight K={k}")
     m = a.rows
@@ -116,9 +126,9 @@ def mx_matmul(activation, weight_fp8, weight_scale, *, epilogue="none", bias=Non
     else:
         width = n // 2 if epi == _native.EPI_SWIGLU else n
         if out is None:
-            out = torch.empty((m, width), device=dev, dtype=torch.bfloat16)
-        if out.dtype != torch.bfloat16 or out.stride(-1) != 1 or out.shape != (m, width):
-            raise ValueError("out must be a bf16 (rows, N) tensor with unit column stride")
+            out = torch.empty((m, width), device=dev, dtype=dtype)
+        if out.dtype != dtype or out.stride(-1) != 1 or out.shape != (m, width):
+            raise ValueError(f"out must be a {dtype} (rows, N) tensor with unit column stride")
         buf, ldo, result = out, out.stride(0), out
     if epi == _native.EPI_GATED_RESIDUAL:
         gate = gate.reshape(-1, n)

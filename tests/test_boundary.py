@@ -193,3 +193,49 @@ def test_qim_attention_backend_applies_only_where_it_can(monkeypatch):
     assert not attention_call._qim_applies(y, y, y, None)                # head dim 64
     out = attention_call.attention(x, x, x)                              # falls back to SDPA on the CPU
     assert out.shape == x.shape and out.dtype == x.dtype
+
+
+# ----------------------------------------------- MXFP8Linear state dicts --
+
+def _quantized_linear(k, n, seed=0):
+    """An MXFP8Linear over random code and scale bytes (no GPU needed)."""
+    from qwen_image_accel.kernels.mxfp8 import padded_rows, tile_codes
+    g = torch.Generator().manual_seed(seed)
+    rows = padded_rows(n)
+    codes = torch.randint(0, 256, (rows, k), generator=g, dtype=torch.uint8).view(torch.float8_e4m3fn)
+    scales = torch.randint(100, 140, (rows * k // 32,), generator=g, dtype=torch.uint8)
+    return mxfp8.MXFP8Linear.from_quantized(k, n, tile_codes(codes), scales), codes
+
+
+@pytest.mark.parametrize("k,n", [(256, 256), (384, 640), (256, 100 * 128)])
+def test_mxfp8linear_state_dict_uses_reference_keys(k, n):
+    """state_dict() holds the reference's weight_fp8 -- the (K, padded N)
+    transpose view of row-major codes -- and weight_scale; it loads back into
+    a fresh module byte for byte, also as a contiguous (K, N) copy (as a
+    safetensors round trip returns it; K = N included, where a transposed
+    load would go unnoticed by shape); a wrong shape is refused."""
+    m, codes = _quantized_linear(k, n)
+    sd = m.state_dict()
+    assert set(sd) == {"weight_fp8", "weight_scale"}
+    assert sd["weight_fp8"].shape == (k, codes.shape[0])
+    assert torch.equal(sd["weight_fp8"].t().view(torch.uint8), codes.view(torch.uint8))
+    for form in (sd["weight_fp8"], sd["weight_fp8"].contiguous()):
+        fresh, _ = _quantized_linear(k, n, seed=1)
+        fresh.load_state_dict({"weight_fp8": form, "weight_scale": sd["weight_scale"]})
+        assert torch.equal(fresh.weight_tiled.view(torch.uint8), m.weight_tiled.view(torch.uint8))
+        assert torch.equal(fresh.weight_scale.view(torch.uint8), m.weight_scale.view(torch.uint8))
+    fresh, _ = _quantized_linear(k, n, seed=1)
+    with pytest.raises(ValueError, match="weight_fp8"):
+        fresh.load_state_dict({"weight_fp8": sd["weight_fp8"][:, :128], "weight_scale": sd["weight_scale"]})
+
+
+def test_conversion_plan_takes_multiples_of_128():
+    """The reference converts a linear when K and N are multiples of 128
+    (optimizations/mxfp8.py:15-16): a 384-wide projection is planned, a
+    320-wide one is not; skipped blocks and the layer selection apply."""
+    t = fq.make_transformer(n_blocks=3, dim=256, heads=2, ffn=512)
+    t.transformer_blocks[1].img_mlp.proj = torch.nn.Linear(256, 384, bias=False)
+    t.transformer_blocks[2].img_mlp.proj = torch.nn.Linear(256, 320, bias=False)
+    plan = mxfp8.conversion_plan(t, skip_blocks="0", layers="img_mlp.proj,attn.to_q")
+    assert [(i, p) for i, p, _ in plan] == [(1, "attn.to_q"), (1, "img_mlp.proj"), (2, "attn.to_q")]
+    assert mxfp8.skipped_blocks("") == set() and mxfp8.skipped_blocks(" 3, 5") == {3, 5}

@@ -573,6 +573,67 @@ def test_mxfp8_gemm_swiglu_epilogues(dev):
     assert np.array_equal(u8(yq.scales), u8(sep.scales))
 
 
+@pytest.mark.parametrize("m,n,k", [(300, 128, 256), (1000, 640, 512), (4352, 3200, 384), (4352, 4224, 256)])
+@pytest.mark.parametrize("epi", ["none", "bias", "gated_residual"])
+def test_mxfp8_gemm_half_width_last_column(dev, m, n, k, epi):
+    """N % 256 == 128 (the reference converts any N % 128 == 0): the last 128
+    columns run as 128 x 128 quarter tiles beside the whole tiles (and, at
+    4352 x 4224, beside the quarter tiles of a partial last round), with
+    row-major and tiled operands.  Sampled rows and all columns against the
+    oracle."""
+    g = torch.Generator().manual_seed(m + n + k)
+    a = bf16_randn(g, (m, k))
+    w = bf16_randn(g, (n, k), 0.05)
+    rows = np.unique(np.concatenate([np.random.default_rng(n).choice(m, 24, replace=False), [0, m - 1]]))
+    kw = {}
+    if epi == "bias":
+        kw["bias"] = bf16_randn(g, (n,), 0.01).to(dev)
+    elif epi == "gated_residual":
+        kw.update(residual=bf16_randn(g, (m, n)).to(dev), gate=bf16_randn(g, (1, 1, n)).tanh().to(dev), seq=m)
+    for tiled in (False, True):
+        say("gemm half column", m, n, k, epi, tiled)
+        aq = mxfp8.quantize(a.to(dev), tiled=tiled)
+        wq = mxfp8.quantize(w.to(dev), tiled=tiled)
+        y = gemm.mx_matmul(aq, wq.values, wq.scales, epilogue=epi, weight_tiled=tiled, **kw)
+        rm_a, rm_w = mxfp8.as_row_major(aq), mxfp8.as_row_major(wq)
+        acc = O.mx_gemm(u8(rm_a.values), u8(rm_a.scales), u8(rm_w.values), u8(rm_w.scales), rows=rows)
+        if epi == "bias":
+            ref = acc + bf16_values(bits(kw["bias"].cpu()))[None, :]
+        elif epi == "gated_residual":
+            res = bf16_values(bits(kw["residual"].cpu()))[rows]
+            ref = res + bf16_values(bits(kw["gate"].cpu())).reshape(1, n) * bf16_values(O.f32_to_bf16(acc))
+            got = bf16_values(bits(y))[rows]
+            assert rel_fro(got - res, ref - res) < 1e-2
+            continue
+        else:
+            ref = acc
+        got = bf16_values(bits(y))[rows]
+        assert rel_fro(got, ref) < 1e-2
+        assert rel_fro(got[:, -128:], ref[:, -128:]) < 1e-2      # the half-width column block
+
+
+@pytest.mark.parametrize("m,n,k", [(300, 512, 256), (4352, 384, 512)])
+def test_mxfp8_gemm_fp32_and_fp16_outputs(dev, m, n, k):
+    """out_dtype of torch._scaled_mm (optimizations/mxfp8.py:34-35): the fp32
+    output against the oracle, and the bf16 and fp16 outputs equal to it
+    rounded (all three come from the same accumulators)."""
+    g = torch.Generator().manual_seed(m + n)
+    a = bf16_randn(g, (m, k))
+    w = bf16_randn(g, (n, k), 0.05)
+    say("gemm out dtypes", m, n, k)
+    aq = mxfp8.quantize(a.to(dev))
+    wq = mxfp8.quantize(w.to(dev))
+    y32 = gemm.mx_matmul(aq, wq.values, wq.scales, dtype=torch.float32)
+    y16 = gemm.mx_matmul(aq, wq.values, wq.scales, dtype=torch.float16)
+    yb = gemm.mx_matmul(aq, wq.values, wq.scales)
+    assert y32.dtype == torch.float32 and y16.dtype == torch.float16 and y32.shape == (m, n)
+    rows = np.random.default_rng(1).choice(m, 32, replace=False)
+    ref = O.mx_gemm(u8(aq.values), u8(aq.scales), u8(wq.values), u8(wq.scales), rows=rows)
+    assert rel_fro(y32.cpu().numpy()[rows], ref) < 1e-2
+    assert torch.equal(y32.to(torch.bfloat16).view(torch.int16), yb.view(torch.int16))
+    assert torch.equal(y32.to(torch.float16).view(torch.int16), y16.view(torch.int16))
+
+
 @pytest.mark.parametrize("m,n,k", [(4352, 4096, 512), (4200, 4096, 384)])
 @pytest.mark.parametrize("epi", ["none", "bias", "gated_residual", "swiglu", "swiglu_quant"])
 def test_mxfp8_gemm_tail_quarter_tiles(dev, m, n, k, epi):

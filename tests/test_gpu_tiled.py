@@ -122,3 +122,29 @@ def test_mxfp8_linear_tiled_weight_and_reference_state_dict(dev):
     want = gemm.mx_matmul(mxfp8.quantize(x.reshape(200, 384)), rowmajor.values, rowmajor.scales)
     assert torch.equal(fresh(x).reshape(200, 512).view(torch.int16), want.view(torch.int16))
     assert torch.equal(mx(x).reshape(200, 512).view(torch.int16), want.view(torch.int16))
+
+
+def test_mxfp8_linear_n_multiple_of_128_and_out_dtype(dev):
+    """A 384-output linear (N % 256 == 128, converted as in the reference):
+    forward equals the row-major GEMM on the same bytes; its state dict (the
+    reference's keys) reloads byte for byte; matmul honours dtype."""
+    say("MXFP8Linear N=384")
+    g = torch.Generator().manual_seed(12)
+    lin = torch.nn.Linear(256, 384, bias=False)
+    with torch.no_grad():
+        lin.weight.copy_(torch.randn(384, 256, generator=g) * 0.05)
+    lin = lin.to(dev, torch.bfloat16)
+    mx = MXFP8Linear(lin)
+    x = bf16_randn(g, (3, 70, 256)).to(dev)
+    rowmajor = mxfp8.quantize(lin.weight.detach().contiguous())
+    a = mxfp8.quantize(x.reshape(210, 256))
+    want = gemm.mx_matmul(a, rowmajor.values, rowmajor.scales)
+    got = mx(x)
+    assert got.shape == (3, 70, 384)
+    assert torch.equal(got.reshape(210, 384).view(torch.int16), want.view(torch.int16))
+    fresh = MXFP8Linear(torch.nn.Linear(256, 384, bias=False).to(dev, torch.bfloat16))
+    fresh.load_state_dict({k: v.contiguous() for k, v in mx.state_dict().items()})
+    assert np.array_equal(u8(fresh.weight_tiled), u8(mx.weight_tiled))
+    y32 = mx.matmul(a, torch.float32)
+    assert y32.dtype == torch.float32
+    assert torch.equal(y32.to(torch.bfloat16).view(torch.int16), want.view(torch.int16))

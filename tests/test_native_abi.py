@@ -52,13 +52,18 @@ def test_abi_version():
     ("qim_adaln", (16, 16, None, None, None, 16, 1, 16392, 1, 1e-6, 0, None), _native.QIM_ERR_SHAPE),
     ("qim_adaln_quantize", (16, 16, None, None, None, 16, 16, 1, 3000, 1, 1e-6, 0, None),
      _native.QIM_ERR_SHAPE),
-    ("qim_mxfp8_gemm", (16, 16, 16, 16, 4, 384, 128, 0, None, None, None, 0, 16, 384, None, None),
+    ("qim_mxfp8_gemm", (16, 16, 16, 16, 4, 320, 128, 0, None, None, None, 0, 16, 320, None, None),
      _native.QIM_ERR_SHAPE),
+    # an fp32 and an fp16 output at once; an fp32 output with the bias epilogue
+    ("qim_mxfp8_gemm_ex", (16, 16, 16, 16, 4, 256, 128, 0, 24, None, None, None, 0, 16, 256, None, None),
+     _native.QIM_ERR_ARG),
+    ("qim_mxfp8_gemm_ex", (16, 16, 16, 16, 4, 256, 128, 1, 8, 16, None, None, 0, 16, 256, None, None),
+     _native.QIM_ERR_ARG),
     ("qim_mxfp8_gemm", (16, 16, 16, 16, 4, 256, 128, 9, None, None, None, 0, 16, 256, None, None),
      _native.QIM_ERR_ARG),
     ("qim_mxfp8_gemm", (16, 16, 16, 16, 4, 256, 128, 2, None, None, None, 0, 16, 256, None, None),
      _native.QIM_ERR_ARG),
-    ("qim_mxfp8_gemm_ex", (16, 16, 16, 16, 4, 256, 128, 0, 8, None, None, None, 0, 16, 256, None, None),
+    ("qim_mxfp8_gemm_ex", (16, 16, 16, 16, 4, 256, 128, 0, 32, None, None, None, 0, 16, 256, None, None),
      _native.QIM_ERR_ARG),
     ("qim_mxfp8_gemm_ex", (16, 16, 16, 16, 4, 256, 128, 0, 4, None, None, None, 0, 16, 256, None, None),
      _native.QIM_ERR_ARG),

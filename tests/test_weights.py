@@ -12,7 +12,7 @@ import torch
 from oracle import oracle as O
 from qwen_image_accel import pipeline, weights
 from qwen_image_accel.kernels import gemm, mxfp8
-from qwen_image_accel.optimizations import mxfp8 as mx, quantized_decode
+from qwen_image_accel.optimizations import decode, mxfp8 as mx
 from tests import fake_qwen21 as fq
 from tests.helpers import bits, swizzle_permute
 
@@ -152,8 +152,8 @@ def test_mxfp8_profile_fused_gate_up_and_prequantized_weights(dev, monkeypatch, 
     cfg, fused = _profile_out(dev, t_fused, inputs)
     assert cfg["mxfp8_fused_gate_up"] == 2 and cfg["mxfp8_fused_qkv"] == 2
     with monkeypatch.context() as m:
-        m.setattr(quantized_decode, "fuse_gate_up", lambda mlp: False)
-        m.setattr(quantized_decode, "fuse_qkv", lambda attn: False)
+        m.setattr(decode, "fuse_gate_up", lambda mlp: False)
+        m.setattr(decode, "fuse_qkv", lambda attn: False)
         cfg_p, plain = _profile_out(dev, t_plain, inputs)
     assert cfg_p["mxfp8_fused_gate_up"] == 0 and cfg_p["mxfp8_fused_qkv"] == 0
     assert torch.equal(fused, plain)
