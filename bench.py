@@ -17,8 +17,13 @@ launch stream, with torch.cuda.synchronize() on both sides.  Bandwidth-bound
 steps rotate through enough copies of their inputs that the working set
 exceeds the 256 MB Infinity Cache, so the figures are HBM figures.
 
-The CPU baseline is this repository's C oracle (a port of the reference's
-eager semantics) run on the host cores of the same box on a bounded sample.
+The GEMM and block steps likewise rotate through enough weight sets (blocks)
+to exceed twice the Infinity Cache, as the 32 blocks of a model stream their
+weights; the "_warm" components keep one set resident, a best case.
+
+The CPU baseline is the reference's eager composition re-expressed as torch
+CPU ops (oracle/eager_torch.py), timed on the host cores of the same box at
+all of this process's cores and at 8 threads, with the C oracle beside it.
 """
 import argparse
 import json
@@ -232,34 +237,47 @@ def bench_quantize(steps, warmup):
                 frac=nbytes / us / 1e3 / HBM_PEAK_GBS, shape="[4352,3072]")
 
 
-def bench_gemm(steps, warmup, tiled=True):
+def bench_gemm(steps, warmup, tiled=True, rotate=True):
     """Config 4b: MXFP8 GEMM [4352 x 3072] x [3072 x 12288] + bias.  ``tiled``:
     both operands in the tiled code layout MXFP8Linear uses (weight quantized
     once, activation quantized with tiled=True); else the reference's
-    row-major codes."""
+    row-major codes.  ``rotate``: the steps cycle through enough distinct
+    (activation, weight, bias, output) sets to exceed twice the Infinity
+    Cache, as a 32-block model streams its weights; else one set stays
+    cache-resident (a warm-cache best case)."""
     from qwen_image_accel import _native
     from qwen_image_accel.kernels import mxfp8
     g = gen(1)
     M, K, N = 4352, 3072, 12288
     a = torch.randn(M, K, generator=g)
     a[torch.rand(M, K, generator=g) < 0.01] *= 20
-    aq = mxfp8.quantize(a.to(torch.bfloat16).cuda(), tiled=tiled)
-    wq = mxfp8.quantize(randn(g, (N, K), 0.02), tiled=tiled)
+    a = a.to(torch.bfloat16).cuda()
+    w = randn(g, (N, K), 0.02)
     bias = randn(g, (N,), 0.01)
-    out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    per_set = M * K + N * K + (M + N) * K // 32 + 2 * M * N + 2 * N
+    n = copies_for(per_set) if rotate else 1
+    # distinct operands of the same distribution: rows rotated per set
+    sets = []
+    for i in range(n):
+        sets.append((mxfp8.quantize(torch.roll(a, 17 * i, 0), tiled=tiled),
+                     mxfp8.quantize(torch.roll(w, 29 * i, 0), tiled=tiled), torch.roll(bias, i),
+                     torch.empty(M, N, dtype=torch.bfloat16, device="cuda")))
     flops = 2 * M * N * K
     L = _native.lib()
     layouts = _native.GEMM_A_TILED | _native.GEMM_B_TILED if tiled else 0
 
     def step(i):
+        aq, wq, bs, out = sets[i % n]
         rc = L.qim_mxfp8_gemm_ex(aq.values.data_ptr(), aq.scales.data_ptr(), wq.values.data_ptr(),
-                                 wq.scales.data_ptr(), M, N, K, _native.EPI_BIAS, layouts, bias.data_ptr(), None,
+                                 wq.scales.data_ptr(), M, N, K, _native.EPI_BIAS, layouts, bs.data_ptr(), None,
                                  None, M, out.data_ptr(), N, None, torch.cuda.current_stream().cuda_stream)
         assert rc == 0
-    us = Timed(step, max(10, steps // 4), warmup).run() * 1e3
+    k_steps = n * max(1, -(-max(10, steps // 4) // n))
+    us = Timed(step, k_steps, warmup).run() * 1e3
     tf = flops / us / 1e6
     return dict(kernel="qim_mxfp8_gemm", us=us, flops=flops, tflops=tf, frac=tf / MXFP8_PEAK_TFLOPS,
-                shape="4352x3072x12288 +bias", layout="tiled" if tiled else "row-major")
+                shape="4352x3072x12288 +bias", layout="tiled" if tiled else "row-major",
+                operand_sets=n, cache="rotated past 2x the Infinity Cache" if rotate else "warm (one set)")
 
 
 def bench_attention(tokens, steps, warmup):
@@ -290,13 +308,26 @@ def bench_attention(tokens, steps, warmup):
                 shape=f"S=T={tokens}, 24x128")
 
 
-def bench_block(tokens, steps, warmup, with_attention=False):
+def bench_block(tokens, steps, warmup, with_attention=False, rotate=True):
     """Config 5 / µs-per-block: one MMDiT block minus the attention core
-    (with_attention: the whole block, the attention core included)."""
+    (with_attention: the whole block, the attention core included).
+    ``rotate``: consecutive steps run different blocks -- enough of them that
+    their MXFP8 weights (151 MB each) exceed twice the Infinity Cache, as the
+    32 blocks of a model follow each other -- else one block, whose weights
+    then stay cache-resident across steps (a warm-cache best case)."""
     from qwen_image_accel import rope
     from qwen_image_accel.block import MMDiTBlock
     g = gen(42)
-    blk = MMDiTBlock.random(g, device="cuda")
+    first = MMDiTBlock.random(g, device="cuda")
+    wbytes = sum(q.values.numel() + q.scales.numel() for q in (first.w_qkv, first.w_out, first.w_gate_up,
+                                                                first.w_down))
+    n = copies_for(wbytes) if rotate else 1
+    blocks = [first]
+    w0 = first.bf16_weights
+    for i in range(1, n):   # distinct weights of the same distribution: rows rotated per block
+        roll = lambda t: torch.roll(t, 31 * i, 0)  # noqa: E731
+        blocks.append(MMDiTBlock.from_weights(roll(w0["qkv"]), roll(w0["out"]), roll(w0["gate"]), roll(w0["up"]),
+                                              roll(w0["down"]), w0["norm_q"], w0["norm_k"], first.heads))
     side = int(round(((tokens - 256)) ** 0.5))
     h = randn(g, (1, tokens, 3072))
     mod = randn(g, (1, 6, 3072), 0.1)
@@ -305,11 +336,13 @@ def bench_block(tokens, steps, warmup, with_attention=False):
     def step(i):
         # with_attention: the library's attention core, V^T written by the QKV
         # projection and the output quantized in the same pass
-        blk.forward(h, mod, freqs, fused_attention=with_attention)
-    us = Timed(step, max(3, steps // 20), warmup).run() * 1e3
-    flops = blk.flops(tokens)
+        blocks[i % n].forward(h, mod, freqs, fused_attention=with_attention)
+    k_steps = n * max(1, -(-max(3, steps // 20) // n))
+    us = Timed(step, k_steps, warmup).run() * 1e3
+    flops = first.flops(tokens)
     return dict(us=us, flops=flops, tflops=flops / us / 1e6, tokens=tokens,
-                gemm_frac=flops / us / 1e6 / MXFP8_PEAK_TFLOPS)
+                gemm_frac=flops / us / 1e6 / MXFP8_PEAK_TFLOPS, blocks=n,
+                cache="weights rotated past 2x the Infinity Cache" if rotate else "warm (one block)")
 
 
 def bench_copy(steps, warmup, n=256 << 20, shape="256 MiB"):
@@ -346,11 +379,81 @@ def measured_traffic(entry):
 
 # ------------------------------------------------------------ CPU baseline --
 
-def cpu_baseline(seconds):
-    """The oracle's fused QK-RMSNorm + RoPE on the config-2 workload, repeated
-    until `seconds` of CPU time, on the host cores (OpenMP)."""
+def cpu_model():
+    """The host CPU's model name (lscpu's "Model name")."""
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def host_cores():
+    """Cores this process may run on, capped at the box's 16-core share per GPU."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+def _median_ms(fn, warmup, repeats):
+    for _ in range(warmup):
+        fn()
+    times = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)) * 1e3
+
+
+def eager_cpu_configs(threads, block_tokens):
+    """The reference's eager composition (oracle/eager_torch.py, torch CPU ops
+    in bf16) of configs 1-4 and of the block, at full size, on `threads`
+    host threads: 3 warm-ups + 10 repeats, median (the GEMM 1 + 3, the block
+    one pass per entry of block_tokens)."""
+    from oracle import eager_torch as E
+    torch.set_num_threads(threads)
+    g = gen(2024)
+    r = lambda *shape, sc=1.0: (torch.randn(shape, generator=g) * sc).to(torch.bfloat16)  # noqa: E731
+    out = {}
+    x, res = r(1, 1280, 3072), r(1, 1280, 3072)
+    sh, sc, ga = (r(1, 1, 3072, sc=0.1) for _ in range(3))
+    out["adaln_512"] = (_median_ms(lambda: E.adaln(x, sc, sh, ga, res), 3, 10), 23611392)
+    q, k = r(1, 4352, 24, 128), r(1, 4352, 24, 128)
+    wn = (torch.rand(128, generator=g) * 0.4 + 0.8).to(torch.bfloat16)
+    fr = torch.polar(torch.ones(4352, 64), torch.rand(4352, 64, generator=g) * 6.28)
+    out["qk_norm_rope_1024"] = (_median_ms(lambda: E.qk_rmsnorm_rope(q, k, wn, wn, fr), 3, 10), 109183488)
+    X = r(4352, 24576)
+    out["swiglu_1024"] = (_median_ms(lambda: E.swiglu(X[:, :12288], X[:, 12288:]), 3, 10), 320864256)
+    h, pj, gt = r(4352, 3072), r(4352, 3072), r(1, 3072, sc=0.1)
+    out["gated_residual_1024"] = (_median_ms(lambda: E.gated_residual(h, pj, gt), 3, 10), 80222208)
+    A = r(4352, 3072)
+    out["quantize_1024"] = (_median_ms(lambda: E.mx_quantize(A), 3, 10), 40525824)
+    W, bias = r(12288, 3072, sc=0.02), r(12288, sc=0.01)
+    qa, qw = E.mx_quantize(A), E.mx_quantize(W)
+    out["mxfp8_gemm_bias_1024"] = (_median_ms(lambda: E.mx_matmul(qa, qw, 4352, bias), 1, 3), None)
+    del X, W
+    if block_tokens:
+        d, f = 3072, 12288
+        wq = {"qkv": E.mx_quantize(r(3 * d, d, sc=0.02)), "out": E.mx_quantize(r(d, d, sc=0.02)),
+              "gate_up": E.mx_quantize(r(2 * f, d, sc=0.02)), "down": E.mx_quantize(r(d, f, sc=0.02))}
+        for tokens in block_tokens:
+            hb, mod = r(1, tokens, d), r(1, 6, d, sc=0.1)
+            frb = torch.polar(torch.ones(tokens, 64), torch.rand(tokens, 64, generator=g) * 6.28)
+            name = {4352: "block_1024", 16640: "block_2048"}[tokens]
+            out[name] = (_median_ms(lambda: E.block(hb, mod, frb, wq, wn, wn, 24), 0, 1), None)
+    return out
+
+
+def oracle_c_baseline(seconds, threads):
+    """The C oracle's fused QK-RMSNorm + RoPE (this build's port of the
+    reference's semantics) on the config-2 workload, repeated for `seconds`."""
     from oracle import oracle as O
-    threads = min(os.cpu_count() or 1, 16)
     O.set_threads(threads)
     rng = np.random.default_rng(721)
     S, H, Dh = 4352, 24, 128
@@ -367,9 +470,41 @@ def cpu_baseline(seconds):
         el = time.perf_counter() - t0
         if el >= seconds or reps >= 10000:
             break
-    return {"value": nbytes * reps / el / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"config-2 workload (Q,K [1,4352,24,128]) x {reps} passes in {el:.1f} s, "
-                      f"C oracle, {threads} OpenMP threads"}
+    return {"value": round(nbytes * reps / el / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"C oracle (oracle/qim_oracle.c, OpenMP), config-2 workload x {reps} passes in {el:.1f} s"}
+
+
+def cpu_baseline(seconds, block_tokens=(4352,)):
+    """The reference's eager path on the host cores: configs 1-4 at all of
+    this process's cores (<= 16) and at 8 threads (the reference's
+    QW21_CPU_THREADS default), the block (one pass per entry of
+    block_tokens) at all cores; the headline value is config 2 at all cores.
+    The block at 16640 tokens (~1 min of CPU) is left out by default to keep
+    the sample bounded."""
+    cores = host_cores()
+    passes = {}
+    for threads in sorted({cores, 8}, reverse=True):
+        log(f"[bench] cpu eager, {threads} threads ...")
+        passes[threads] = eager_cpu_configs(threads, block_tokens if threads == cores else ())
+    configs = {}
+    for name in passes[cores]:
+        entry = {}
+        for threads, res in passes.items():
+            if name in res:
+                ms, nbytes = res[name]
+                entry[f"ms_{threads}t"] = round(ms, 3)
+                if nbytes:
+                    entry[f"GBs_{threads}t"] = round(nbytes / ms / 1e6, 2)
+        configs[name] = entry
+    ms2 = passes[cores]["qk_norm_rope_1024"][0]
+    torch.set_num_threads(cores)
+    return {"value": round(109183488 / ms2 / 1e6, 2), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": "config 2 (Q,K [1,4352,24,128]) by the reference's eager composition as torch CPU ops in "
+                      f"bf16 (oracle/eager_torch.py), median of 10 after 3 warm-ups, {cores} threads; every "
+                      "config also at 8 threads under 'configs' (GEMM: median of 3; blocks: one pass, "
+                      "all cores only)",
+            "cpu_model": cpu_model(), "os_cpu_count": os.cpu_count(), "configs": configs,
+            "oracle_c": oracle_c_baseline(seconds, cores)}
 
 
 def main():
@@ -377,7 +512,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=5.0)
+    ap.add_argument("--cpu-block", default="4352",
+                    help="token counts of the blocks in the CPU baseline (comma list; '' = none; 16640 ~ 1 min)")
     ap.add_argument("--only", default="", help="comma list of components (debug)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -401,8 +538,10 @@ def main():
                      ("gated_residual_1024", lambda: bench_residual(steps, warm)),
                      ("quantize_1024", lambda: bench_quantize(steps, warm)),
                      ("mxfp8_gemm_bias_1024", lambda: bench_gemm(steps, warm)),
+                     ("mxfp8_gemm_bias_1024_warm", lambda: bench_gemm(steps, warm, rotate=False)),
                      ("mxfp8_gemm_bias_1024_rowmajor", lambda: bench_gemm(steps, warm, tiled=False)),
                      ("block_1024", lambda: bench_block(4352, steps, warm)),
+                     ("block_1024_warm", lambda: bench_block(4352, steps, warm, rotate=False)),
                      ("block_2048", lambda: bench_block(16640, steps, warm)),
                      ("attention_1024", lambda: bench_attention(4352, steps, warm)),
                      ("attention_2048", lambda: bench_attention(16640, steps, warm)),
@@ -463,7 +602,8 @@ def main():
     out["components"] = summary
     if want("cpu"):
         log("[bench] cpu baseline ...")
-        out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        out["cpu_baseline"] = cpu_baseline(args.cpu_seconds,
+                                           tuple(int(t) for t in args.cpu_block.split(",") if t.strip()))
     print(json.dumps(out), flush=True)
 
 
