@@ -258,10 +258,12 @@ __device__ __forceinline__ float rstd_of(float var, float eps) {
 // The sum of squares is taken in float64: for bf16 inputs it is exact, so it
 // does not depend on how the lanes of a row are reduced; it is rounded once to
 // the fp32 mean.
+// (The square of a bf16 value is exact in float64, so the fused multiply-add
+// rounds exactly as a multiply then an add would.)
 __device__ __forceinline__ double head_sumsq8(const float *x) {
     double ss = 0.0;
 #pragma unroll
-    for (int t = 0; t < 8; ++t) ss += (double)x[t] * (double)x[t];
+    for (int t = 0; t < 8; ++t) ss = __builtin_fma((double)x[t], (double)x[t], ss);
     return ss;
 }
 // x: the chunk; ss: the row's total sum of squares over `width` values; w: the

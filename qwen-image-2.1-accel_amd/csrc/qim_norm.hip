@@ -345,34 +345,39 @@ __global__ __launch_bounds__(256) void k_norm_rope(NormRopeArgs p) {
     const int lane = threadIdx.x & 63;
     const int g = lane / LPR, c = lane % LPR;
     if ((int64_t)blockIdx.x < p.main_blocks) {
-        const uint32_t w = blockIdx.x * 4u + (threadIdx.x >> 6);
+        // The work item is wave-uniform: computed in scalar registers (the
+        // divisions run on the scalar unit); a lane adds only its own offset
+        // g * D + c * 8 inside the item's run of head rows.
+        const uint32_t w = blockIdx.x * 4u + (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
         if (w >= p.main_waves) return;  // whole wave
         const uint32_t per_token = NTENS * p.groups;
         const uint32_t t = w / per_token;
         const uint32_t r = w - t * per_token;
-        const uint32_t tensor = r / p.groups;  // wave-uniform
-        const int h0 = (int)(r - tensor * p.groups) * (RPI * U) + g;
+        const uint32_t tensor = r / p.groups;
+        const int hb = (int)(r - tensor * p.groups) * (RPI * U);  // first head of the item
+        const int h0 = hb + g;
         const int H = (int)p.H;
         const uint32_t bb = t / (uint32_t)p.S, tok = t - bb * (uint32_t)p.S;
-        const uint16_t *src = (tensor == 0 ? p.q : tensor == 1 ? p.k : p.v) + (int64_t)t * p.ldt + c * 8;
+        const uint16_t *src = (tensor == 0 ? p.q : tensor == 1 ? p.k : p.v) + (int64_t)t * p.ldt + (int64_t)hb * D;
         uint16_t *dst;
         if (tensor == 0) {
-            dst = p.oq + (int64_t)t * H * D + c * 8;
+            dst = p.oq + ((int64_t)t * H + hb) * D;
         } else {
-            const int64_t kv_row = ((int64_t)bb * (p.P + p.S) + p.P + tok) * H;
-            dst = (tensor == 1 ? p.ok : p.ov) + kv_row * D + c * 8;
+            const int64_t kv_row = ((int64_t)bb * (p.P + p.S) + p.P + tok) * H + hb;
+            dst = (tensor == 1 ? p.ok : p.ov) + kv_row * D;
         }
+        const int off = g * D + c * 8;  // this lane's elements within the item
         uint4 x[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int h = h0 + u * RPI;
-            if (FULL || h < H) x[u] = ld_nt(src + (int64_t)h * D);
+            if (FULL || h < H) x[u] = ld_nt(src + off + u * RPI * D);
         }
         if (NTENS == 3 && tensor == 2) {
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const int h = h0 + u * RPI;
-                if (FULL || h < H) st_nt(dst + (int64_t)h * D, x[u]);
+                if (FULL || h < H) st_nt(dst + off + u * RPI * D, x[u]);
             }
             return;
         }
@@ -388,7 +393,7 @@ __global__ __launch_bounds__(256) void k_norm_rope(NormRopeArgs p) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int h = h0 + u * RPI;
-            if (FULL || h < H) st_nt(dst + (int64_t)h * D, norm_rope_chunk<LPR, NORM, ROPE>(x[u], wt, eps, f0, f1));
+            if (FULL || h < H) st_nt(dst + off + u * RPI * D, norm_rope_chunk<LPR, NORM, ROPE>(x[u], wt, eps, f0, f1));
         }
     } else if constexpr (NTENS == 3) {
         // Prefix copy: B * P * H rows of D, RPI rows per wave instruction.
