@@ -271,6 +271,12 @@ int qim_debug_silu(const void *g, void *out, int64_t n, void *stream);
  * bandwidth reference of the benchmarks and the calibration kernel of the HBM
  * byte counters.  No reference counterpart. */
 int qim_debug_copy(const void *src, void *dst, int64_t nbytes, void *stream);
+/* Variants of that copy for the single-launch bandwidth ceiling:
+ * vectors_per_lane (1, 2, 4, 8) 16-byte vectors per lane, loads before
+ * stores; blocks_per_cu = 0: one-shot grid covering nbytes, else a
+ * persistent grid of blocks_per_cu workgroups per CU striding over it. */
+int qim_debug_copy_ex(const void *src, void *dst, int64_t nbytes, int vectors_per_lane, int blocks_per_cu,
+                      void *stream);
 
 #ifdef __cplusplus
 }

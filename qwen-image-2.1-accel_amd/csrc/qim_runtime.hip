@@ -169,9 +169,57 @@ __global__ __launch_bounds__(256) void k_debug_copy(const uint4 *__restrict__ sr
     if (i < nvec) st_nt(dst + i, ld_nt(src + i));
 }
 
+// Copy variants for the single-launch bandwidth ceiling: U 16-byte vectors
+// per lane (all loads, then all stores); one-shot (each workgroup one chunk of
+// 256 U vectors) or grid-stride over a persistent grid.
+template <int U, bool PERSIST>
+__global__ __launch_bounds__(256) void k_debug_copy_u(const uint4 *__restrict__ src, uint4 *__restrict__ dst,
+                                                       int64_t nvec) {
+    const int64_t stride = PERSIST ? (int64_t)gridDim.x * 256 * U : nvec;
+    for (int64_t base = (int64_t)blockIdx.x * 256 * U + threadIdx.x; base < nvec; base += stride) {
+        uint4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            if (base + u * 256 < nvec) v[u] = ld_nt(src + base + u * 256);
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            if (base + u * 256 < nvec) st_nt(dst + base + u * 256, v[u]);
+    }
+}
+
 }  // namespace qim
 
 using namespace qim;
+
+extern "C" int qim_debug_copy_ex(const void *src, void *dst, int64_t nbytes, int vectors_per_lane, int blocks_per_cu,
+                                 void *stream) {
+    QIM_REQUIRE(src && dst && nbytes >= 0 && blocks_per_cu >= 0 && blocks_per_cu <= 64, QIM_ERR_ARG,
+                "qim_debug_copy_ex: bad arguments");
+    QIM_REQUIRE(vectors_per_lane == 1 || vectors_per_lane == 2 || vectors_per_lane == 4 || vectors_per_lane == 8,
+                QIM_ERR_ARG, "qim_debug_copy_ex: vectors_per_lane must be 1, 2, 4 or 8");
+    QIM_REQUIRE(nbytes % 16 == 0 && aligned16(src) && aligned16(dst), QIM_ERR_LAYOUT,
+                "qim_debug_copy_ex: 16-byte aligned operands and size required");
+    const int64_t nvec = nbytes / 16, per_block = 256ll * vectors_per_lane;
+    QIM_REQUIRE(nvec / per_block < (1ll << 31), QIM_ERR_SHAPE, "qim_debug_copy_ex: too large");
+    if (nvec == 0) return QIM_OK;
+    const int cus = device_cus() > 0 ? device_cus() : 256;
+    const int64_t grid = blocks_per_cu ? (int64_t)blocks_per_cu * cus : (nvec + per_block - 1) / per_block;
+    const uint4 *s = (const uint4 *)src;
+    uint4 *d = (uint4 *)dst;
+    hipStream_t st = as_stream(stream);
+    const dim3 g((unsigned)grid), b(256);
+    switch (vectors_per_lane * 2 + (blocks_per_cu ? 1 : 0)) {
+        case 2: launch(k_debug_copy_u<1, false>, g, b, 0, st, s, d, nvec); break;
+        case 3: launch(k_debug_copy_u<1, true>, g, b, 0, st, s, d, nvec); break;
+        case 4: launch(k_debug_copy_u<2, false>, g, b, 0, st, s, d, nvec); break;
+        case 5: launch(k_debug_copy_u<2, true>, g, b, 0, st, s, d, nvec); break;
+        case 8: launch(k_debug_copy_u<4, false>, g, b, 0, st, s, d, nvec); break;
+        case 9: launch(k_debug_copy_u<4, true>, g, b, 0, st, s, d, nvec); break;
+        case 16: launch(k_debug_copy_u<8, false>, g, b, 0, st, s, d, nvec); break;
+        default: launch(k_debug_copy_u<8, true>, g, b, 0, st, s, d, nvec); break;
+    }
+    return check_launch("qim_debug_copy_ex");
+}
 
 extern "C" int qim_debug_silu(const void *g, void *out, int64_t n, void *stream) {
     QIM_REQUIRE(g && out && n >= 0, QIM_ERR_ARG, "qim_debug_silu: bad arguments");

@@ -70,6 +70,7 @@ SIGNATURES = {
     "qim_debug_mfma_tile": (_C, [_P, _P, _P, _P, _P, _P]),
     "qim_debug_mfma_probe": (_C, [_C, _P, _P]),
     "qim_debug_copy": (_C, [_P, _P, _I, _P]),
+    "qim_debug_copy_ex": (_C, [_P, _P, _I, _C, _C, _P]),
     "qim_debug_silu": (_C, [_P, _P, _I, _P]),
 }
 

@@ -122,7 +122,8 @@ def test_silu_exhaustive(dev):
 
 
 def test_streaming_copy(dev):
-    """The bandwidth/counter calibration copy moves every byte, tail included."""
+    """The bandwidth/counter calibration copy and its ceiling variants move
+    every byte, tails included, and nothing past the end."""
     n = (3 << 20) + 48
     say("copy", n)
     src = torch.randint(0, 256, (n,), dtype=torch.uint8).to(dev)
@@ -130,6 +131,13 @@ def test_streaming_copy(dev):
     _native.call("qim_debug_copy", _native.ptr(src), _native.ptr(dst), n, _native.stream())
     got = dst.cpu()
     assert torch.equal(got[:n], src.cpu()) and int(got[n:].sum()) == 0
+    for vpl in (1, 2, 4, 8):
+        for bpc in (0, 1, 4):
+            say("copy_ex", vpl, bpc)
+            dst.zero_()
+            _native.call("qim_debug_copy_ex", _native.ptr(src), _native.ptr(dst), n, vpl, bpc, _native.stream())
+            got = dst.cpu()
+            assert torch.equal(got[:n], src.cpu()) and int(got[n:].sum()) == 0, (vpl, bpc)
 
 
 # ---------------------------------------------------------------- quantize --
