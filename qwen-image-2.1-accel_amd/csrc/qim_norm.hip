@@ -27,6 +27,7 @@ struct AdaLNArgs {
     float eps;
     int flags;
     int tiled;         // quantized codes in the GEMM's tiled layout (mxt_offset over rows_pad rows)
+    double inv_d;      // fl(1 / D), set by launch_adaln
 };
 
 // Byte offset of codes [8j, 8j + 8) of a quantized row.
@@ -40,6 +41,28 @@ constexpr int ADALN_FULL_WAVES = 4;    // full-coverage kernels: 256 threads, no
 // bf16x2 words of the neutral operand of each optional step: adding -0 and
 // multiplying by 1 return a bf16 value unchanged (signed zeros included).
 constexpr uint32_t BF16X2_NEG_ZERO = 0x80008000u, BF16X2_ONE = 0x3f803f80u;
+
+// The biased variance of a row, rounded to fp32, from one pass: S2 = sum(x^2)
+// and mean_d = fl(S1 / D).  The reference value is fl32(fl(V / D)), V the
+// float64 two-pass sum of (x - mean_d)^2 in any order.  Both that value and
+// v1 = S2 / D - mean_d^2 (evaluated below) lie within
+//   E = (2D + 32) 2^-53 (|v1| + mean_d^2) (1 + 2^-20)
+// of sum((x - mean_d)^2) / D: the two-pass sum of D positive terms, each
+// rounded three times, is within (D + 3) 2^-53 of it relatively; S2 (D - 1
+// additions of exact squares), the product by fl(1/D), mean_d^2 and the
+// subtraction give (D + 2) 2^-53 of the variance plus (D + 4) 2^-53 of
+// mean^2.  When v1 - E and v1 + E round to the same fp32 value, so does the
+// reference value (rounding is monotonic), and it is returned; otherwise
+// (false) the caller runs the second pass.  NaN or infinite sums give a NaN
+// interval end, which compares unequal.
+__device__ __forceinline__ bool ln_variance(double s2, double mean_d, int D, double inv_d, float &var) {
+    const double sq = mean_d * mean_d;
+    const double v1 = s2 * inv_d - sq;
+    const double e = (2.0 * D + 32.0) * 0x1p-53 * (__builtin_fabs(v1) + sq) * (1.0 + 0x1p-20);
+    const float lo = (float)(v1 - e), hi = (float)(v1 + e);
+    var = lo;
+    return lo == hi;
+}
 
 // One modulated LayerNorm row per workgroup of W waves (reference chain, eager
 // rounding points: t0 = bf16(LN x), t1 = scale or bf16(1 + scale),
@@ -58,7 +81,7 @@ constexpr uint32_t BF16X2_NEG_ZERO = 0x80008000u, BF16X2_ONE = 0x3f803f80u;
 // arithmetic: with gate 1 and residual -0 those steps return t3 unchanged.
 template <bool QUANT, int NV, bool FULL, bool RG>
 __global__ __launch_bounds__(FULL ? 64 * ADALN_FULL_WAVES : 64 * ADALN_MAX_WAVES) void k_adaln(AdaLNArgs p) {
-    __shared__ double red[2][FULL ? ADALN_FULL_WAVES : ADALN_MAX_WAVES];
+    __shared__ double red[3][FULL ? ADALN_FULL_WAVES : ADALN_MAX_WAVES];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nthr = blockDim.x, nw = nthr >> 6;
     const int64_t row = blockIdx.x;
@@ -142,38 +165,70 @@ __global__ __launch_bounds__(FULL ? 64 * ADALN_FULL_WAVES : 64 * ADALN_MAX_WAVES
 #pragma unroll
     for (int i = 0; i < NV; ++i) unpack8(xv[i], x[i]);
 
-    // Row statistics in float64: the sum of the row's bf16 values is exact (it
-    // does not depend on the reduction order); the mean and the biased
-    // variance (two passes) are rounded once to fp32.  Absent vectors hold
-    // zeros and add nothing.
-    double s = 0.0;
+    // Row statistics in float64 (the reference statistics: mean = fp32(S1/D)
+    // with S1 the exact float64 sum of the row's bf16 values, and the biased
+    // variance fp32(sum((x - mean_d)^2) / D) of a second pass).  One pass
+    // gathers S1 and S2 = sum(x^2) (each square exact, so the FMA rounds as
+    // the sum would); ln_variance decides the variance's fp32 rounding from
+    // them when it can, else (a rare row: var near an fp32 rounding midpoint,
+    // or cancellation) the second pass runs.  Absent vectors hold zeros.
+    double s1 = 0.0, s2 = 0.0;
 #pragma unroll
     for (int i = 0; i < NV; ++i)
 #pragma unroll
-        for (int t = 0; t < 8; ++t) s += (double)x[i][t];
-    s = wave_total(s);
-    if (lane == 0) red[0][wave] = s;
-    __syncthreads();
-    s = 0.0;
-    for (int w = 0; w < nw; ++w) s += red[0][w];
-    const double mean_d = s / (double)p.D;
-    double ss = 0.0;
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const bool ok = FULL || tid + nthr * i < nvec;
-#pragma unroll
         for (int t = 0; t < 8; ++t) {
-            const double d = ok ? (double)x[i][t] - mean_d : 0.0;
-            ss += d * d;
+            const double v = (double)x[i][t];
+            s1 += v;
+            s2 = __builtin_fma(v, v, s2);
+        }
+    s1 = wave_total(s1);
+    s2 = wave_total(s2);
+    if (lane == 0) {
+        red[0][wave] = s1;
+        red[1][wave] = s2;
+    }
+    if constexpr (FULL) {
+        // The slots of absent waves hold +0, which leaves the sums unchanged,
+        // so every wave adds the four slots in one fixed order.
+        static_assert(ADALN_FULL_WAVES == 4, "the cross-wave sums add four slots");
+        if (wave == 0 && lane >= nw && lane < ADALN_FULL_WAVES) {
+            red[0][lane] = 0.0;
+            red[1][lane] = 0.0;
+        }
+        __syncthreads();
+        s1 = (red[0][0] + red[0][1]) + (red[0][2] + red[0][3]);
+        s2 = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+    } else {
+        __syncthreads();
+        s1 = 0.0;
+        s2 = 0.0;
+        for (int w = 0; w < nw; ++w) {
+            s1 += red[0][w];
+            s2 += red[1][w];
         }
     }
-    ss = wave_total(ss);
-    if (lane == 0) red[1][wave] = ss;
-    __syncthreads();
-    ss = 0.0;
-    for (int w = 0; w < nw; ++w) ss += red[1][w];
+    const double mean_d = s1 / (double)p.D;
+    float var;
+    if (!ln_variance(s2, mean_d, p.D, p.inv_d, var)) {  // uniform over the workgroup
+        double ss = 0.0;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const bool ok = FULL || tid + nthr * i < nvec;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const double d = ok ? (double)x[i][t] - mean_d : 0.0;
+                ss += d * d;
+            }
+        }
+        ss = wave_total(ss);
+        if (lane == 0) red[2][wave] = ss;
+        __syncthreads();
+        ss = 0.0;
+        for (int w = 0; w < nw; ++w) ss += red[2][w];
+        var = (float)(ss / (double)p.D);
+    }
     const float mean = (float)mean_d;
-    const float rstd = rstd_of((float)(ss / (double)p.D), p.eps);
+    const float rstd = rstd_of(var, p.eps);
     // t1 = bf16(scale + 1) with add_one, else scale (+ -0 leaves it unchanged).
     const float scale_add = (p.flags & QIM_ADALN_ADD_ONE) ? 1.0f : -0.0f;
     if constexpr (LATE) load_scale_shift();
@@ -284,7 +339,8 @@ static int launch_adaln_rg(const AdaLNArgs &a, hipStream_t st) {
 }
 
 template <bool QUANT>
-static int launch_adaln(const AdaLNArgs &a, hipStream_t st) {
+static int launch_adaln(AdaLNArgs a, hipStream_t st) {
+    a.inv_d = 1.0 / (double)a.D;
     return (a.res || a.gate) ? launch_adaln_rg<QUANT, true>(a, st) : launch_adaln_rg<QUANT, false>(a, st);
 }
 

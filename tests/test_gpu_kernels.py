@@ -263,6 +263,38 @@ def test_layer_norm_scale_quantize(dev, b, n, d):
     assert np.array_equal(u8(fused.scales), sc)
 
 
+def _rows_with_offsets(g, rows, d):
+    """Rows whose mean is large against their spread (mean/std up to ~1e3)
+    and near-constant rows: the one-pass variance cannot settle the fp32
+    rounding for most of them, so the kernels' second pass runs, beside rows
+    where it settles it."""
+    x = bf16_randn(g, (1, rows, d))
+    offset = torch.tensor([0.0, 1.0, 8.0, 30.0, 100.0, 1e3])[torch.arange(rows) % 6]
+    x = (x.float() + offset[None, :, None]).to(torch.bfloat16)
+    x[0, 5::17] = 3.0
+    x[0, 5::17, ::301] = 3.5
+    return x
+
+
+@pytest.mark.parametrize("d", [3072, 4096])
+def test_adaln_second_pass_rows(dev, d):
+    """The config-1 chain and the quantizing AdaLN on rows that take the
+    second statistics pass: bit-exact against the oracle's two-pass float64
+    statistics."""
+    g = torch.Generator().manual_seed(d + 5)
+    x = _rows_with_offsets(g, 300, d)
+    shift, scale, gate = (bf16_randn(g, (1, 1, d), 0.1) for _ in range(3))
+    res = bf16_randn(g, (1, 300, d))
+    say("adaln second pass", d)
+    out = layernorm.layer_norm_scale(x.to(dev), scale.to(dev), _LN(d), shift=shift.to(dev),
+                                     gate=gate.to(dev), residual=res.to(dev), add_one=True)
+    assert_bits_equal(bits(out), O.adaln(bits(x), bits(scale), bits(shift), bits(gate), bits(res), add_one=True))
+    fused = epilogue.layer_norm_scale_quantize(x.to(dev), scale.to(dev), _LN(d))
+    q, sc = O.adaln_quantize(bits(x), bits(scale))
+    assert np.array_equal(u8(fused.values), q)
+    assert np.array_equal(u8(fused.scales), sc)
+
+
 # --------------------------------------------------- residual, SwiGLU --
 
 @pytest.mark.parametrize("b,s,d", [(1, 49, 4096), (2, 257, 4096), (1, 4352, 3072)])
