@@ -259,6 +259,9 @@ int qim_attention_noalloc(const void *q, int64_t ldq, const void *k, int64_t ldk
  * out (32, 32) fp32 = sum_k a*2^(sa-127) b*2^(sb-127). */
 int qim_debug_e4m3_encode(const float *x, void *codes, int64_t n, void *stream);
 int qim_debug_bf16_round(const float *x, void *bits, int64_t n, void *stream);
+/* bf16 x (n % 4 == 0, 16-byte aligned) -> E4M3 codes of x * 2^(127 - e), 0 <= e <= 254, through the
+ * packed scaled conversion (v_cvt_scalef32_pk_fp8_bf16) the quantizers use. */
+int qim_debug_e4m3_encode_scaled(const void *x, int e, void *codes, int64_t n, void *stream);
 int qim_debug_mfma_tile(const void *a, const void *b, const void *sa, const void *sb,
                         float *out, void *stream);
 /* Scale-routing probe of the scaled MFMA (shape 0: 32x32x64, 1: 16x16x128):

@@ -539,12 +539,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                 const uint32_t mp = (uint32_t)__shfl_xor((int)m, 32, 64);
                 m = mp > m ? mp : m;
                 const int e = mx_exponent(__uint_as_float(m));
-                const float ie = mx_inverse(e);
+                const float s = mx_scale_operand(e);
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const int64_t k = (int64_t)h * ATT_D + 32 * dt + 8 * g + 4 * hf;
                     *reinterpret_cast<uint32_t *>(p.qcodes + att_code_offset(p, row, k)) =
-                        cvt_e4m3x4(f[4 * g] * ie, f[4 * g + 1] * ie, f[4 * g + 2] * ie, f[4 * g + 3] * ie);
+                        cvt_e4m3x4_scaled(f[4 * g], f[4 * g + 1], f[4 * g + 2], f[4 * g + 3], s);
                 }
                 sc |= (uint32_t)e << (8 * dt);
             }

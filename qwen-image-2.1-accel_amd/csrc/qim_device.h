@@ -93,6 +93,34 @@ __device__ __forceinline__ uint32_t cvt_e4m3x4(float a, float b, float c, float 
     return (uint32_t)r;
 }
 
+// Scaled conversions (v_cvt_scalef32_pk_fp8_f32 / _bf16): E4M3 RNE of
+// x / 2^(E - 127), E the exponent field of the fp32 scale operand (its
+// mantissa is ignored; a field of 0 means 2^-127).  With the scale operand
+// e << 23 they give the codes of x * 2^(127 - e), i.e. of x * mx_inverse(e),
+// without the multiply; the bf16 form also takes its two inputs packed.
+// Measured on MI355X over every bf16 input: equal to the oracle's E4M3 RNE of
+// x * 2^(127 - e) wherever that is at most 448 in magnitude, for e = 0 (scale
+// operand 0.0f), 1, 127 and 254; non-finite and out-of-range inputs convert as
+// v_cvt_pk_fp8_f32 converts them.
+typedef short i16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float mx_scale_operand(int e) { return __uint_as_float((uint32_t)e << 23); }
+
+// Four fp32 values a..d -> four codes (bytes 0..3) of v / 2^(e - 127).
+__device__ __forceinline__ uint32_t cvt_e4m3x4_scaled(float a, float b, float c, float d, float scale) {
+    i16x2_t r = {0, 0};
+    r = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(r, a, b, scale, false);
+    r = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(r, c, d, scale, true);
+    return __builtin_bit_cast(uint32_t, r);
+}
+
+// Two packed bf16 pairs (low half first) -> four codes (bytes 0..3).
+__device__ __forceinline__ uint32_t cvt_e4m3x4_bf16(uint32_t ab, uint32_t cd, float scale) {
+    i16x2_t r = {0, 0};
+    r = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(r, __builtin_bit_cast(bf16x2_t, ab), scale, false);
+    r = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(r, __builtin_bit_cast(bf16x2_t, cd), scale, true);
+    return __builtin_bit_cast(uint32_t, r);
+}
+
 // Byte offset of the E8M0 exponent of (row r, block kb) of a (rows, K) tensor
 // in the 128x4 swizzled layout (kernels/mxfp8.py:53-56).
 __device__ __forceinline__ int64_t mx_scale_offset(int64_t r, int64_t kb, int64_t K) {
@@ -314,11 +342,33 @@ __device__ __forceinline__ uint2 quantize8(const float *f, int &e) {
     uint32_t m = absmax_bits8(f);
     m = group_umax<4>(m);
     e = mx_exponent(__uint_as_float(m));
-    float inv = mx_inverse(e);
+    const float s = mx_scale_operand(e);
     uint2 c;
-    c.x = cvt_e4m3x4(f[0] * inv, f[1] * inv, f[2] * inv, f[3] * inv);
-    c.y = cvt_e4m3x4(f[4] * inv, f[5] * inv, f[6] * inv, f[7] * inv);
+    c.x = cvt_e4m3x4_scaled(f[0], f[1], f[2], f[3], s);
+    c.y = cvt_e4m3x4_scaled(f[4], f[5], f[6], f[7], s);
     return c;
+}
+
+// fp32 bits of the largest magnitude among 8 packed bf16 values: the
+// magnitudes as unsigned 16-bit halves (their order is the values' order,
+// NaN above everything) through packed 16-bit maxima, widened to fp32 bits --
+// the same as absmax_bits8 of the unpacked values.
+__device__ __forceinline__ uint32_t absmax_bits_bf16x8(const uint4 &u) {
+    typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+    const u16x2_t a = __builtin_bit_cast(u16x2_t, u.x & 0x7fff7fffu), b = __builtin_bit_cast(u16x2_t, u.y & 0x7fff7fffu);
+    const u16x2_t c = __builtin_bit_cast(u16x2_t, u.z & 0x7fff7fffu), d = __builtin_bit_cast(u16x2_t, u.w & 0x7fff7fffu);
+    const u16x2_t m = __builtin_elementwise_max(__builtin_elementwise_max(a, b), __builtin_elementwise_max(c, d));
+    const uint32_t hi = m.y, lo = m.x;
+    return (hi > lo ? hi : lo) << 16;
+}
+
+// quantize8 of 8 packed bf16 values (one 16-byte vector): the same codes and
+// exponent as quantize8 of the unpacked values, without unpacking them.
+__device__ __forceinline__ uint2 quantize8_bf16(const uint4 &u, int &e) {
+    uint32_t m = group_umax<4>(absmax_bits_bf16x8(u));
+    e = mx_exponent(__uint_as_float(m));
+    const float s = mx_scale_operand(e);
+    return make_uint2(cvt_e4m3x4_bf16(u.x, u.y, s), cvt_e4m3x4_bf16(u.z, u.w, s));
 }
 
 // ------------------------------------------------------------- math ----

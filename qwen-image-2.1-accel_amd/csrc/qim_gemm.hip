@@ -562,14 +562,8 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
                 const int64_t grow = row0 + half * 64 + 4 * g + r;
                 const uint4 v = rowv[r];
                 if constexpr (EPI == QIM_EPI_SWIGLU_QUANT) {
-                    float f[8];
-                    unpack8(v, f);
-                    const uint32_t m = group_umax<4>(absmax_bits8(f));
-                    const int e = mx_exponent(__uint_as_float(m));
-                    const float inv = mx_inverse(e);
-                    uint2 c;
-                    c.x = cvt_e4m3x4(f[0] * inv, f[1] * inv, f[2] * inv, f[3] * inv);
-                    c.y = cvt_e4m3x4(f[4] * inv, f[5] * inv, f[6] * inv, f[7] * inv);
+                    int e;
+                    const uint2 c = quantize8_bf16(v, e);
                     if (grow < p.Mp) {
                         const int64_t o = p.out_tiled ? mxt_offset(grow, col, p.Mp, F) : grow * F + col;
                         st_nt(reinterpret_cast<uint8_t *>(p.out) + o, c);

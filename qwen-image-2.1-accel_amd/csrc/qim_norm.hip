@@ -278,12 +278,8 @@ __global__ __launch_bounds__(FULL ? 64 * ADALN_FULL_WAVES : 64 * ADALN_MAX_WAVES
             }
             // A 32-element block is 4 adjacent lanes; 4 adjacent blocks (16
             // lanes) own one dword of the swizzled scale array.
-            const uint32_t m = group_umax<4>(absmax_bits8(o));
-            const int e = mx_exponent(__uint_as_float(m));
-            const float inv = mx_inverse(e);
-            uint2 c;
-            c.x = cvt_e4m3x4(o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv);
-            c.y = cvt_e4m3x4(o[4] * inv, o[5] * inv, o[6] * inv, o[7] * inv);
+            int e;
+            const uint2 c = quantize8(o, e);
             st_nt(p.q + adaln_code_offset(p, row, j), c);
             const uint32_t e1 = (uint32_t)__shfl((int)e, lane + 4, 64);
             const uint32_t e2 = (uint32_t)__shfl((int)e, lane + 8, 64);

@@ -1,12 +1,14 @@
 // MXFP8 quantizers: quantize(x) and the fused swiglu_quantize(g, v).
 //
-// One workgroup quantizes one 128-row x 128-column tile, the unit of the
+// The unit of work is a 128-row x 128-column tile, the unit of the
 // reference's scale layout: its 512 E8M0 bytes form one contiguous chunk of
-// the swizzled scale array, so they are staged in LDS and written with 32
-// 16-byte stores.  Each wave owns 32 rows of the tile; 16 lanes cover one
-// 128-column row (8 bf16 = one 16-byte load per lane), 4 rows per pass,
-// 8 passes.  A 32-element block is 4 adjacent lanes, reduced with two DPP
-// quad permutes.  All 8 loads of a lane are issued before any arithmetic.
+// the swizzled scale array.  A wave owns 32 rows of a tile; 16 lanes cover
+// one 128-column row (8 bf16 = one 16-byte load per lane), 4 rows per pass,
+// 8 passes, loads two passes at a time.  A 32-element block is 4 adjacent
+// lanes, reduced with two DPP quad permutes; the codes come from the packed
+// bf16 values through the scaled conversion (no unpacking, no multiply).  A
+// wave's 32 x 4 exponents are staged in LDS and written one dword per row.
+// Workgroups are one wave (a quarter tile; measured fastest at config 4a).
 // HBM traffic is the algorithmic minimum: every input byte read once, every
 // code and scale byte written once.  Codes are written row-major or in the
 // GEMM's tiled layout (mxt_offset); an 8-byte store stays contiguous in both.
@@ -19,13 +21,21 @@ namespace qim {
 struct QuantSource {
     const uint16_t *x;
     int64_t ldx;
-    __device__ __forceinline__ void load(bool live, int64_t row, int64_t col, uint4 &a, uint4 &b) const {
-        a = live ? ld_nt(x + row * ldx + col) : make_uint4(0, 0, 0, 0);
+    // Loads of rows row + 4i (i = 0..7) at column col: pointer and step set once.
+    const uint16_t *px;
+    int64_t step;
+    __device__ __forceinline__ void start(int64_t row, int64_t col) {
+        px = x + row * ldx + col;
+        step = 4 * ldx;
+    }
+    __device__ __forceinline__ void load(bool live, int i, uint4 &a, uint4 &b) const {
+        a = live ? ld_nt(px + i * step) : make_uint4(0, 0, 0, 0);
         (void)b;
     }
-    __device__ __forceinline__ void values(const uint4 &a, const uint4 &b, float *f) const {
+    // The 8 bf16 values as they are: converted packed, no unpacking.
+    __device__ __forceinline__ uint2 quantize(const uint4 &a, const uint4 &b, int &e) const {
         (void)b;
-        unpack8(a, f);
+        return quantize8_bf16(a, e);
     }
 };
 
@@ -37,60 +47,93 @@ struct SwigluSource {
     int64_t ldg;
     const uint16_t *v;
     int64_t ldv;
-    __device__ __forceinline__ void load(bool live, int64_t row, int64_t col, uint4 &a, uint4 &b) const {
-        a = live ? ld_nt(g + row * ldg + col) : make_uint4(0, 0, 0, 0);
-        b = live ? ld_nt(v + row * ldv + col) : make_uint4(0, 0, 0, 0);
+    const uint16_t *pg, *pv;
+    int64_t sg, sv;
+    __device__ __forceinline__ void start(int64_t row, int64_t col) {
+        pg = g + row * ldg + col;
+        pv = v + row * ldv + col;
+        sg = 4 * ldg;
+        sv = 4 * ldv;
     }
-    __device__ __forceinline__ void values(const uint4 &a, const uint4 &b, float *f) const {
-        float gg[8], vv[8], s[8];
+    __device__ __forceinline__ void load(bool live, int i, uint4 &a, uint4 &b) const {
+        a = live ? ld_nt(pg + i * sg) : make_uint4(0, 0, 0, 0);
+        b = live ? ld_nt(pv + i * sv) : make_uint4(0, 0, 0, 0);
+    }
+    __device__ __forceinline__ uint2 quantize(const uint4 &a, const uint4 &b, int &e) const {
+        float gg[8], vv[8], s[8], f[8];
         unpack8(a, gg);
         unpack8(b, vv);
         silu_bf16_n<8>(gg, s);
 #pragma unroll
         for (int i = 0; i < 8; ++i) f[i] = rbf(s[i] * vv[i]);
+        return quantize8(f, e);
     }
 };
 
-template <class Source>
-__global__ __launch_bounds__(256) void k_quant_tile(Source src, uint8_t *__restrict__ q,
-                                                     uint8_t *__restrict__ scales, int64_t M,
-                                                     int64_t K, int tiled) {
-    __shared__ uint4 s_scale[32];  // the tile's 512 swizzled exponent bytes
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+// W waves per workgroup.  W = 4: one workgroup per 128 x 128 tile; W = 1:
+// one per 32-row quarter of it (wave role = blockIdx.x % 4), so a launch has
+// four times as many workgroups and the last round of the CUs is fuller.
+template <class Source, int W>
+__global__ __launch_bounds__(64 * W) void k_quant_tile(Source src, uint8_t *__restrict__ q,
+                                                        uint8_t *__restrict__ scales, int64_t M,
+                                                        int64_t K, int tiled) {
+    __shared__ uint32_t s_scale[W][32];  // per wave: row r % 32 -> its 4 exponent bytes
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = W == 1 ? (int)(blockIdx.x & 3) : tid >> 6;
     const int c16 = lane & 15;    // 8-column chunk of the 128-column tile row
     const int rsub = lane >> 4;   // row within a pass of 4 rows
-    const int64_t row0 = (int64_t)blockIdx.x * 128;
+    const int64_t row0 = (int64_t)(W == 1 ? blockIdx.x >> 2 : blockIdx.x) * 128;
     const int64_t col = (int64_t)blockIdx.y * 128 + c16 * 8;
-    uint8_t *sb = reinterpret_cast<uint8_t *>(s_scale);
+    uint8_t *sb = reinterpret_cast<uint8_t *>(s_scale[W == 1 ? 0 : wave]);
+    // This lane's rows are rb + 4i (i = 0..7) of the tile; their addresses
+    // advance by a fixed step, computed once.
+    const int rb = wave * 32 + rsub;
+    Source in = src;
+    in.start(row0 + rb, col);
 
+    // Loads in flight per lane: two rows at a time (all eight at once crowds
+    // the L1 miss queue: measured slower).
     uint4 a[8], b[8];
+    // Code offsets: row-major (row0 + r) * K + col; tiled (mxt_offset) the
+    // 256-row super-block's slab of col plus 64 bytes per row and the row's
+    // chunk swizzle -- the lane's 8 rows share the super-block.
+    const int64_t Mp = (int64_t)gridDim.x * (W == 1 ? 32 : 128);
+    const int64_t r0 = (row0 + rb) & ~int64_t(255);
+    const int64_t n = Mp - r0 < 256 ? Mp - r0 : 256;
+    const int64_t out0 = tiled ? r0 * K + (col >> 6) * n * 64 + (col & 15) : (row0 + rb) * K + col;
+    const int rl = (int)(row0 + rb - r0), chunk = (int)((col >> 4) & 3);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const int r = wave * 32 + i * 4 + rsub;
-        src.load(row0 + r < M, row0 + r, col, a[i], b[i]);
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int r = wave * 32 + i * 4 + rsub;  // r / 32 == wave
-        float f[8];
-        src.values(a[i], b[i], f);
+        if ((i & 1) == 0) {
+            in.load(row0 + rb + 4 * i < M, i, a[i], b[i]);
+            in.load(row0 + rb + 4 * i + 4 < M, i + 1, a[i + 1], b[i + 1]);
+        }
         int e;
-        uint2 c = quantize8(f, e);
-        const int64_t Mp = (int64_t)gridDim.x * 128;
-        st_nt(q + (tiled ? mxt_offset(row0 + r, col, Mp, K) : (row0 + r) * K + col), c);
-        if ((c16 & 3) == 0) sb[(r & 31) * 16 + wave * 4 + (c16 >> 2)] = (uint8_t)e;
+        const uint2 c = in.quantize(a[i], b[i], e);
+        const int rr = rl + 4 * i;
+        st_nt(q + out0 + (tiled ? (int64_t)(rr * 64 + ((chunk ^ mx_chunk_swizzle(rr)) << 4)) : i * 4 * K), c);
+        if ((c16 & 3) == 0) sb[(rsub + 4 * i) * 4 + (c16 >> 2)] = (uint8_t)e;
     }
     __syncthreads();
-    if (tid < 32) {
-        uint4 *dst = reinterpret_cast<uint4 *>(scales + ((int64_t)blockIdx.x * (K >> 7) + blockIdx.y) * 512);
-        dst[tid] = s_scale[tid];
+    // The tile's 512 scale bytes: row r (of 128) at (r % 32) * 16 + (r / 32) * 4;
+    // each wave's 32 rows are one dword per 16 bytes.
+    uint8_t *chunk0 = scales + ((int64_t)(row0 >> 7) * (K >> 7) + blockIdx.y) * 512;
+    if (W == 1) {
+        if (lane < 32) *reinterpret_cast<uint32_t *>(chunk0 + lane * 16 + wave * 4) = s_scale[0][lane];
+    } else if (tid < 32) {
+        *reinterpret_cast<uint4 *>(chunk0 + tid * 16) =
+            make_uint4(s_scale[0][tid], s_scale[W > 1 ? 1 : 0][tid], s_scale[W > 2 ? 2 : 0][tid], s_scale[W > 3 ? 3 : 0][tid]);
     }
 }
+
+// Workgroups of one wave (W = 1) or four (W = 4): the launch shape of the
+// quantizers.
+constexpr int QUANT_WAVES = 1;
 
 static int launch_quant_checks(const char *what, int64_t M, int64_t K) {
     QIM_REQUIRE(M > 0 && K > 0, QIM_ERR_SHAPE, "%s: empty input (M=%lld, K=%lld)", what, (long long)M, (long long)K);
     QIM_REQUIRE(K % 128 == 0, QIM_ERR_SHAPE, "%s: K=%lld is not a multiple of 128", what, (long long)K);
-    QIM_REQUIRE((M + 127) / 128 < (1ll << 31) && K / 128 < 65536, QIM_ERR_SHAPE, "%s: too large", what);
+    QIM_REQUIRE((M + 127) / 128 * 4 < (1ll << 31) && K / 128 < 65536, QIM_ERR_SHAPE, "%s: too large", what);
     return QIM_OK;
 }
 
@@ -105,9 +148,9 @@ static int mx_quantize(const void *x, int64_t ldx, int64_t M, int64_t K, void *q
     if (rc) return rc;
     QIM_REQUIRE(ldx >= K && ldx % 8 == 0 && aligned16(x) && aligned16(q) && aligned16(scales), QIM_ERR_LAYOUT,
                 "qim_mx_quantize: x must be 16-byte aligned with ldx %% 8 == 0 (ldx=%lld)", (long long)ldx);
-    dim3 grid((unsigned)((M + 127) / 128), (unsigned)(K / 128));
+    dim3 grid((unsigned)((M + 127) / 128 * (4 / QUANT_WAVES)), (unsigned)(K / 128));
     QuantSource src{(const uint16_t *)x, ldx};
-    launch(k_quant_tile<QuantSource>, grid, dim3(256), 0, as_stream(stream), src, (uint8_t *)q,
+    launch(k_quant_tile<QuantSource, QUANT_WAVES>, grid, dim3(64 * QUANT_WAVES), 0, as_stream(stream), src, (uint8_t *)q,
                        (uint8_t *)scales, M, K, tiled);
     return check_launch("qim_mx_quantize");
 }
@@ -120,9 +163,9 @@ static int swiglu_quantize(const void *g, int64_t ldg, const void *v, int64_t ld
     QIM_REQUIRE(ldg >= F && ldv >= F && ldg % 8 == 0 && ldv % 8 == 0 && aligned16(g) && aligned16(v) &&
                     aligned16(q) && aligned16(scales),
                 QIM_ERR_LAYOUT, "qim_swiglu_quantize: inputs must be 16-byte aligned with strides %% 8 == 0");
-    dim3 grid((unsigned)((M + 127) / 128), (unsigned)(F / 128));
+    dim3 grid((unsigned)((M + 127) / 128 * (4 / QUANT_WAVES)), (unsigned)(F / 128));
     SwigluSource src{(const uint16_t *)g, ldg, (const uint16_t *)v, ldv};
-    launch(k_quant_tile<SwigluSource>, grid, dim3(256), 0, as_stream(stream), src, (uint8_t *)q,
+    launch(k_quant_tile<SwigluSource, QUANT_WAVES>, grid, dim3(64 * QUANT_WAVES), 0, as_stream(stream), src, (uint8_t *)q,
                        (uint8_t *)scales, M, F, tiled);
     return check_launch("qim_swiglu_quantize");
 }

@@ -68,6 +68,13 @@ __global__ void k_debug_e4m3(const float *__restrict__ x, uint8_t *__restrict__ 
     }
 }
 
+// bf16 values (n % 4 == 0) -> E4M3 codes of x * 2^(127 - e) through the packed
+// scaled conversion the quantizers use.
+__global__ void k_debug_e4m3_scaled(const uint32_t *__restrict__ x, int e, uint32_t *__restrict__ codes, int64_t n4) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n4) codes[i] = cvt_e4m3x4_bf16(x[2 * i], x[2 * i + 1], mx_scale_operand(e));
+}
+
 __global__ void k_debug_bf16(const float *__restrict__ x, uint16_t *__restrict__ bits, int64_t n) {
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) bits[i] = (uint16_t)(pack_bf16x2(x[i], 0.0f) & 0xffffu);
@@ -262,6 +269,16 @@ extern "C" int qim_debug_e4m3_encode(const float *x, void *codes, int64_t n, voi
     launch(k_debug_e4m3, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
                        as_stream(stream), x, (uint8_t *)codes, n);
     return check_launch("qim_debug_e4m3_encode");
+}
+
+extern "C" int qim_debug_e4m3_encode_scaled(const void *x, int e, void *codes, int64_t n, void *stream) {
+    QIM_REQUIRE(x && codes && n >= 0 && n % 4 == 0 && e >= 0 && e <= 254 && aligned16(x) && aligned16(codes),
+                QIM_ERR_ARG, "qim_debug_e4m3_encode_scaled: bad arguments");
+    if (n == 0) return QIM_OK;
+    const int64_t n4 = n / 4;
+    launch(k_debug_e4m3_scaled, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, as_stream(stream),
+           (const uint32_t *)x, e, (uint32_t *)codes, n4);
+    return check_launch("qim_debug_e4m3_encode_scaled");
 }
 
 extern "C" int qim_debug_bf16_round(const float *x, void *bits, int64_t n, void *stream) {

@@ -66,6 +66,7 @@ SIGNATURES = {
     "qim_attention_mxfp8": (_C, [_P, _I, _P, _I, _P, _I, _P, _P, _C, _P, _I, _I, _I, _I, _I, _I, _F, _P]),
     "qim_attention_noalloc": (_C, [_P, _I, _P, _I, _P, _I, _P, _I, _I, _I, _I, _I, _I, _F, _P]),
     "qim_debug_e4m3_encode": (_C, [_P, _P, _I, _P]),
+    "qim_debug_e4m3_encode_scaled": (_C, [_P, _C, _P, _I, _P]),
     "qim_debug_bf16_round": (_C, [_P, _P, _I, _P]),
     "qim_debug_mfma_tile": (_C, [_P, _P, _P, _P, _P, _P]),
     "qim_debug_mfma_probe": (_C, [_C, _P, _P]),

@@ -59,6 +59,27 @@ def test_e4m3_hardware_conversion_exhaustive(dev):
     assert bad.size == 0, [(float(v[i]), int(got[i]), int(ref[i])) for i in bad[:10]]
 
 
+@pytest.mark.parametrize("e", [0, 1, 100, 119, 127, 134, 200, 254])
+def test_e4m3_scaled_conversion_exhaustive(dev, e):
+    """The packed scaled conversion every quantizer uses
+    (v_cvt_scalef32_pk_fp8_bf16 with the E8M0 exponent e in the scale
+    operand) == oracle RNE of x * 2^(127 - e), on every bf16 x for which that
+    is at most 448 in magnitude -- the only values the quantizers convert
+    (their exponent rule guarantees it).  e = 0 is the scale operand 0.0."""
+    raw = np.arange(65536, dtype=np.uint16)
+    with np.errstate(invalid="ignore", over="ignore"):
+        y = bf16_values(raw).astype(np.float64) * 2.0 ** (127 - e)
+        ok = np.isfinite(y) & (np.abs(y) <= 448)
+    say("e4m3 scaled exhaustive", e, int(ok.sum()))
+    x = torch.from_numpy(raw.view(np.int16)).to(dev)
+    out = torch.empty(65536, dtype=torch.uint8, device=dev)
+    _native.call("qim_debug_e4m3_encode_scaled", _native.ptr(x), e, _native.ptr(out), 65536, _native.stream())
+    got = out.cpu().numpy()
+    ref = O.e4m3_encode(np.where(ok, y, 0.0).astype(np.float32))
+    bad = np.where(ok & (got != ref))[0]
+    assert bad.size == 0, [(hex(raw[i]), int(got[i]), int(ref[i])) for i in bad[:10]]
+
+
 def test_bf16_hardware_rounding(dev):
     """v_cvt_pk_bf16_f32 == oracle RNE, subnormals included."""
     rng = np.random.default_rng(1)

@@ -68,6 +68,9 @@ def test_abi_version():
     ("qim_mxfp8_gemm_ex", (16, 16, 16, 16, 4, 256, 128, 0, 4, None, None, None, 0, 16, 256, None, None),
      _native.QIM_ERR_ARG),
     ("qim_mx_quantize_tiled", (16, 128, 1, 100, 16, 16, None), _native.QIM_ERR_SHAPE),
+    # scaled-conversion hook: exponent 255; n not a multiple of 4
+    ("qim_debug_e4m3_encode_scaled", (16, 255, 16, 64, None), _native.QIM_ERR_ARG),
+    ("qim_debug_e4m3_encode_scaled", (16, 127, 16, 66, None), _native.QIM_ERR_ARG),
     ("qim_qk_norm_rope_pack", (16, 16, None, None, None, 16, 16, 16, 16, 16, None, 1, 4, 3, 2, 128,
                                256, 1e-6, 1e-6, None), _native.QIM_ERR_ARG),
     # attention: head dim 64; scale 0; a workspace smaller than the problem needs; misaligned q
