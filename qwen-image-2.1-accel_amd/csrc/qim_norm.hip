@@ -79,7 +79,14 @@ __device__ __forceinline__ bool ln_variance(double s2, double mean_d, int D, dou
 // RG: the call has a residual or a gate.  Without them (the block's
 // LN * (1 + scale) + shift) the kernel skips their loads, registers and
 // arithmetic: with gate 1 and residual -0 those steps return t3 unchanged.
-template <bool QUANT, int NV, bool FULL, bool RG>
+// ALL: shift, residual and gate are all present (config 1's chain): their
+// loads are unconditional and issued in the order x, gate, scale, shift,
+// residual.  The loads' counter drains in issue order, and loads under a
+// branch make every later wait assume the fewest outstanding loads, so with
+// the optional-operand branches the statistics waited for the residual too;
+// here they wait for x alone, the chain for the column vectors, and only the
+// final add for the residual (the last loads).
+template <bool QUANT, int NV, bool FULL, bool RG, bool ALL = false>
 __global__ __launch_bounds__(FULL ? 64 * ADALN_FULL_WAVES : 64 * ADALN_MAX_WAVES) void k_adaln(AdaLNArgs p) {
     __shared__ double red[3][FULL ? ADALN_FULL_WAVES : ADALN_MAX_WAVES];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -114,6 +121,32 @@ __global__ __launch_bounds__(FULL ? 64 * ADALN_FULL_WAVES : 64 * ADALN_MAX_WAVES
         const bool ok = FULL || j < nvec;
         xv[i] = ok ? ld_nt(xr + j) : zero;
     }
+    static_assert(!ALL || (RG && !QUANT), "the all-operand form is the bf16 chain with residual and gate");
+    if constexpr (ALL) {
+        const uint4 *ga = reinterpret_cast<const uint4 *>(p.gate + (int64_t)b * p.D);
+        const uint4 *sh = reinterpret_cast<const uint4 *>(p.shift + (int64_t)b * p.D);
+        const uint4 *rr = reinterpret_cast<const uint4 *>(p.res + row * p.D);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int j = tid + nthr * i;
+            gv[i] = (FULL || j < nvec) ? ga[j] : one;
+        }
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int j = tid + nthr * i;
+            sv[i] = (FULL || j < nvec) ? sc[j] : zero;
+        }
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int j = tid + nthr * i;
+            hv[i] = (FULL || j < nvec) ? sh[j] : neg0;
+        }
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int j = tid + nthr * i;
+            rv[i] = (FULL || j < nvec) ? ld_nt(rr + j) : neg0;
+        }
+    }
     // The per-batch scale and shift vectors (L2-resident, shared by every row)
     // are loaded with x in the bf16-output kernel and after the statistics in
     // the quantizing one, where the shorter live range lowers the register
@@ -138,28 +171,30 @@ __global__ __launch_bounds__(FULL ? 64 * ADALN_FULL_WAVES : 64 * ADALN_MAX_WAVES
             for (int i = 0; i < NV; ++i) hv[i] = neg0;
         }
     };
-    if constexpr (!LATE) load_scale_shift();
-    if (RG && p.res) {
-        const uint4 *rr = reinterpret_cast<const uint4 *>(p.res + row * p.D);
+    if constexpr (!LATE && !ALL) load_scale_shift();
+    if constexpr (!ALL) {
+        if (RG && p.res) {
+            const uint4 *rr = reinterpret_cast<const uint4 *>(p.res + row * p.D);
 #pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            const int j = tid + nthr * i;
-            rv[i] = (FULL || j < nvec) ? ld_nt(rr + j) : neg0;
+            for (int i = 0; i < NV; ++i) {
+                const int j = tid + nthr * i;
+                rv[i] = (FULL || j < nvec) ? ld_nt(rr + j) : neg0;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < NV; ++i) rv[i] = neg0;
         }
-    } else {
+        if (RG && p.gate) {
+            const uint4 *ga = reinterpret_cast<const uint4 *>(p.gate + (int64_t)b * p.D);
 #pragma unroll
-        for (int i = 0; i < NV; ++i) rv[i] = neg0;
-    }
-    if (RG && p.gate) {
-        const uint4 *ga = reinterpret_cast<const uint4 *>(p.gate + (int64_t)b * p.D);
+            for (int i = 0; i < NV; ++i) {
+                const int j = tid + nthr * i;
+                gv[i] = (FULL || j < nvec) ? ga[j] : one;
+            }
+        } else {
 #pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            const int j = tid + nthr * i;
-            gv[i] = (FULL || j < nvec) ? ga[j] : one;
+            for (int i = 0; i < NV; ++i) gv[i] = one;
         }
-    } else {
-#pragma unroll
-        for (int i = 0; i < NV; ++i) gv[i] = one;
     }
     float x[NV][8];
 #pragma unroll
@@ -308,6 +343,12 @@ static int launch_adaln_rg(const AdaLNArgs &a, hipStream_t st) {
         // quantizing 15.3 vs 17.0 us (4352 rows), bf16 with residual and gate
         // 7.92 vs 7.76 us (1280 rows).
         if (!QUANT && k % 2 == 0 && k / 2 <= ADALN_FULL_WAVES) {
+            if constexpr (!QUANT && RG) {
+                if (a.shift && a.res && a.gate) {  // the full chain: loads without branches
+                    launch((k_adaln<false, 2, true, true, true>), grid, dim3(64 * (k / 2)), 0, st, a);
+                    return QIM_OK;
+                }
+            }
             launch((k_adaln<QUANT, 2, true, RG>), grid, dim3(64 * (k / 2)), 0, st, a);
             return QIM_OK;
         }
