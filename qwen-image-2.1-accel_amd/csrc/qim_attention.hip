@@ -715,7 +715,7 @@ int attention_run(const char *who, const void *q, int64_t ldq, const void *k, in
     QIM_REQUIRE(workspace_bytes >= pl.total(), QIM_ERR_ARG,
                 "%s: workspace of %lld bytes, this problem needs %lld (qim_attention_workspace_bytes)", who,
                 (long long)workspace_bytes, (long long)pl.total());
-    static bool configured[2][QIM_MAX_DEVICES] = {};
+    static std::atomic<bool> configured[2][QIM_MAX_DEVICES] = {};
     const void *fwd = qcodes ? reinterpret_cast<const void *>(&k_attn_fwd<true>)
                              : reinterpret_cast<const void *>(&k_attn_fwd<false>);
     if (const int rc = reserve_lds(fwd, ATT_LDS, configured[qcodes ? 1 : 0], who)) return rc;

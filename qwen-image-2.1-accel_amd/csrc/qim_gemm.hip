@@ -791,7 +791,7 @@ static int64_t main_tile_count(int64_t tiles) {
 
 template <int EPI>
 static int launch_gemm(const GemmArgs &a, hipStream_t st) {
-    static bool configured[QIM_MAX_DEVICES] = {};
+    static std::atomic<bool> configured[QIM_MAX_DEVICES] = {};
     if (const int rc = reserve_lds(reinterpret_cast<const void *>(&k_mx_gemm<EPI>), LDS_BYTES, configured,
                                    "qim_mxfp8_gemm"))
         return rc;

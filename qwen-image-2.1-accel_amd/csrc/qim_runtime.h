@@ -1,6 +1,7 @@
 // Host-side helpers of the libqim C ABI: error reporting and argument checks.
 #pragma once
 
+#include <atomic>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -55,7 +56,7 @@ int device_cus();
 // the attribute is set once per device and kernel.  QIM_OK, or
 // QIM_ERR_LAUNCH with a message naming `who`.
 constexpr int QIM_MAX_DEVICES = 64;
-int reserve_lds(const void *fn, int bytes, bool (&done)[QIM_MAX_DEVICES], const char *who);
+int reserve_lds(const void *fn, int bytes, std::atomic<bool> (&done)[QIM_MAX_DEVICES], const char *who);
 
 }  // namespace qim
 

@@ -33,25 +33,30 @@ int check_launch(const char *what) {
     return QIM_OK;
 }
 
+// Per-device caches are written by whichever thread calls first; the values
+// written are the same from every thread, so relaxed atomics suffice.
 int device_cus() {
-    static int cached[QIM_MAX_DEVICES] = {0};
+    static std::atomic<int> cached[QIM_MAX_DEVICES] = {};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
-    if (dev < QIM_MAX_DEVICES && cached[dev]) return cached[dev];
+    if (dev < QIM_MAX_DEVICES) {
+        const int c = cached[dev].load(std::memory_order_relaxed);
+        if (c) return c;
+    }
     int n = 0;
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    if (dev < QIM_MAX_DEVICES) cached[dev] = n;
+    if (dev < QIM_MAX_DEVICES) cached[dev].store(n, std::memory_order_relaxed);
     return n;
 }
 
-int reserve_lds(const void *fn, int bytes, bool (&done)[QIM_MAX_DEVICES], const char *who) {
+int reserve_lds(const void *fn, int bytes, std::atomic<bool> (&done)[QIM_MAX_DEVICES], const char *who) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0) return fail(QIM_ERR_LAUNCH, "%s: no current device", who);
-    if (dev < QIM_MAX_DEVICES && done[dev]) return QIM_OK;
+    if (dev < QIM_MAX_DEVICES && done[dev].load(std::memory_order_relaxed)) return QIM_OK;
     const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
     if (e != hipSuccess)
         return fail(QIM_ERR_LAUNCH, "%s: cannot reserve %d bytes of LDS: %s", who, bytes, hipGetErrorString(e));
-    if (dev < QIM_MAX_DEVICES) done[dev] = true;
+    if (dev < QIM_MAX_DEVICES) done[dev].store(true, std::memory_order_relaxed);
     return QIM_OK;
 }
 
