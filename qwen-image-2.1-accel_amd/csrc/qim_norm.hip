@@ -272,13 +272,17 @@ __global__ __launch_bounds__(FULL ? 64 * ADALN_FULL_WAVES : 64 * ADALN_MAX_WAVES
     for (int i = 0; i < NV; ++i) {
         const int j = tid + nthr * i;
         if (!FULL && j >= nvec) break;  // uniform inside each 16-lane group when D % 128 == 0
-        float sf[8], hf[8], gf[8], rf[8], o[8];
+        float sf[8], hf[8], gf[8], rf[8];
         unpack8(sv[i], sf);
         unpack8(hv[i], hf);
         if constexpr (RG) {
             unpack8(gv[i], gf);
             unpack8(rv[i], rf);
         }
+        // The output's last rounding (t3 without residual and gate, out with
+        // them) packs two values per dword and stays packed: it is what the
+        // bf16 store writes and what the quantizer reads.
+        uint32_t ow[4];
 #pragma unroll
         for (int t = 0; t < 8; t += 2) {
             float a0 = (x[i][t] - mean) * rstd, a1 = (x[i][t + 1] - mean) * rstd;
@@ -290,31 +294,24 @@ __global__ __launch_bounds__(FULL ? 64 * ADALN_FULL_WAVES : 64 * ADALN_MAX_WAVES
             rbf2(a0, a1);                                             // t2
             a0 += hf[t];
             a1 += hf[t + 1];
-            rbf2(a0, a1);                                             // t3
             if constexpr (RG) {
+                rbf2(a0, a1);                                         // t3
                 a0 *= gf[t];
                 a1 *= gf[t + 1];
                 rbf2(a0, a1);                                         // t4
-                o[t] = rf[t] + a0;
-                o[t + 1] = rf[t + 1] + a1;
+                ow[t / 2] = pack_bf16x2(rf[t] + a0, rf[t + 1] + a1);  // out
             } else {
-                o[t] = a0;
-                o[t + 1] = a1;
+                ow[t / 2] = pack_bf16x2(a0, a1);                      // t3
             }
         }
+        const uint4 packed = make_uint4(ow[0], ow[1], ow[2], ow[3]);
         if constexpr (!QUANT) {
-            st_nt(reinterpret_cast<uint4 *>(p.out + row * p.D) + j, pack8(o));
+            st_nt(reinterpret_cast<uint4 *>(p.out + row * p.D) + j, packed);
         } else {
-            if constexpr (RG) {
-                rbf2(o[0], o[1]);
-                rbf2(o[2], o[3]);
-                rbf2(o[4], o[5]);
-                rbf2(o[6], o[7]);
-            }
             // A 32-element block is 4 adjacent lanes; 4 adjacent blocks (16
             // lanes) own one dword of the swizzled scale array.
             int e;
-            const uint2 c = quantize8(o, e);
+            const uint2 c = quantize8_bf16(packed, e);
             st_nt(p.q + adaln_code_offset(p, row, j), c);
             const uint32_t e1 = (uint32_t)__shfl((int)e, lane + 4, 64);
             const uint32_t e2 = (uint32_t)__shfl((int)e, lane + 8, 64);
