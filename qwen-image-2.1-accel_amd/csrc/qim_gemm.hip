@@ -24,6 +24,8 @@
 // issued at the top of stage s, right after the barrier that proves every wave
 // has consumed ring slot s % 4; the fragments of stage s+1 are read from LDS
 // while the 16 MFMAs of stage s run.
+#include <type_traits>
+
 #include "qim_device.h"
 #include "qim_runtime.h"
 
@@ -411,6 +413,10 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
         // The residual rows of this half's pass 2, loaded before pass 1 so that
         // their latency overlaps it (rows past M: clamped, not stored).
         [[maybe_unused]] uint4 rpre[16 / GPI][4];
+        // The gate vector of this half's rows when they are one batch's (a
+        // per-row load in pass 2 would sit between stores: see pass 2).
+        [[maybe_unused]] uint4 gpre = make_uint4(0, 0, 0, 0);
+        [[maybe_unused]] bool gate_once = false;
         if constexpr (EPI == QIM_EPI_GATED_RESIDUAL) {
             const int cl = lane % LPR, gl = lane / LPR;
 #pragma unroll
@@ -421,6 +427,10 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
                     grow = grow < p.M ? grow : p.M - 1;
                     rpre[it][r] = ld_nt(p.res + grow * p.N + col0 + cl * 8);
                 }
+            const int64_t h0 = row0 + half * 64, h1 = (h0 + 63 < p.M ? h0 + 63 : p.M - 1);
+            const int64_t b0 = (h0 < p.M ? h0 : p.M - 1) / p.seq;
+            gate_once = b0 == h1 / p.seq;
+            gpre = *reinterpret_cast<const uint4 *>(p.gate + b0 * p.N + col0 + cl * 8);
         }
         // pass 1
 #pragma unroll
@@ -494,7 +504,39 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
             }
             continue;
         }
+        // Pass 2.  Loads issued between one row group's stores and the next
+        // group's use would make the compiler wait for those stores too (the
+        // vector-memory counter drains in issue order and counts stores), and
+        // a per-row "row < M" branch makes every wait after it assume the
+        // fewest outstanding operations.  So: the per-half gate vector and the
+        // head weights are loaded before the loop, the QK epilogue's RoPE
+        // rows one row group ahead (before the current group's stores), and a
+        // half whose 64 rows are all below M takes a version of the loop
+        // without per-row checks (every half, when M % 64 == 0).
         const int cl = lane % LPR, gl = lane / LPR;
+        const int64_t col = col0 + cl * 8;
+        [[maybe_unused]] const bool isq = col0 < p.q_cols;
+        [[maybe_unused]] const int hc = (int)(col0 & 127) + cl * 8;  // column within the head
+        [[maybe_unused]] float wt[8];
+        [[maybe_unused]] float4 fr[2][4][2];  // RoPE (cos, sin) of 4 rows: this group's and the next's
+        [[maybe_unused]] const bool qk_cols = is_qk_epi<EPI>() && col0 < p.qk_cols;
+        auto load_freqs = [&](int it, float4 (&f)[4][2]) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t tok = (uint32_t)(row0 + half * 64 + 4 * (it * GPI + gl) + r) % (uint32_t)p.seq;
+                const float4 *fp = reinterpret_cast<const float4 *>(p.freqs + (int64_t)tok * 128 + hc);
+                f[r][0] = fp[0];
+                f[r][1] = fp[1];
+            }
+        };
+        if constexpr (is_qk_epi<EPI>()) {
+            if (qk_cols) {
+                unpack8(*reinterpret_cast<const uint4 *>((isq ? p.wq : p.wk) + hc), wt);
+                load_freqs(0, fr[0]);
+            }
+        }
+        auto pass2 = [&](auto all_rows, auto one_gate) {
+            constexpr bool ALL_ROWS = decltype(all_rows)::value, ONE_GATE = decltype(one_gate)::value;
 #pragma unroll
         for (int it = 0; it < 16 / GPI; ++it) {
             const int g = it * GPI + gl;  // row group: rows 4g .. 4g+3 of this half
@@ -515,7 +557,6 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
 #pragma unroll
                 for (int r = 0; r < 4; ++r) rowv[r] = make_uint4(w[r][0], w[r][1], w[r][2], w[r][3]);
             }
-            const int64_t col = col0 + cl * 8;
             if constexpr (is_qk_epi<EPI>()) {
                 // Q and K head columns: RMSNorm + RoPE of each row's 128-wide
                 // head, as k_norm_rope computes it on the stored output.  A
@@ -524,12 +565,9 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
                 // whose row sums come through LDS.  The Q/K/V class is uniform
                 // over a quarter tile's four waves (one head), so its barriers
                 // are too.
-                if (col0 < p.qk_cols) {
-                    const bool isq = col0 < p.q_cols;
-                    const int hc = (int)(col0 & 127) + cl * 8;  // column within the head
-                    float wt[8], x[4][8];
+                if (qk_cols) {
+                    float x[4][8];
                     double ss[4];
-                    unpack8(*reinterpret_cast<const uint4 *>((isq ? p.wq : p.wk) + hc), wt);
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         unpack8(rowv[r], x[r]);
@@ -549,12 +587,11 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
                     const float eps = isq ? p.epsq : p.epsk;
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const uint32_t tok = (uint32_t)(row0 + half * 64 + 4 * g + r) % (uint32_t)p.seq;
-                        const float4 *fr = reinterpret_cast<const float4 *>(p.freqs + (int64_t)tok * 128 + hc);
                         head_rmsnorm8(x[r], ss[r], 128, eps, wt);
-                        head_rope8(x[r], fr[0], fr[1]);
+                        head_rope8(x[r], fr[it & 1][r][0], fr[it & 1][r][1]);
                         rowv[r] = pack8(x[r]);
                     }
+                    if (it + 1 < 16 / GPI) load_freqs(it + 1, fr[(it + 1) & 1]);
                 }
             }
 #pragma unroll
@@ -570,11 +607,12 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
                         if ((cl & 3) == 0) p.out_scales[mx_scale_offset(grow, col >> 5, F)] = (uint8_t)e;
                     }
                 } else {
-                    if (grow >= p.M) continue;
+                    if (!ALL_ROWS && grow >= p.M) continue;
                     uint4 o = v;
                     if constexpr (EPI == QIM_EPI_GATED_RESIDUAL) {
                         const uint4 hv = rpre[it][r];
-                        const uint4 gv = *reinterpret_cast<const uint4 *>(p.gate + (grow / p.seq) * p.N + col);
+                        const uint4 gv = ONE_GATE ? gpre
+                                                  : *reinterpret_cast<const uint4 *>(p.gate + (grow / p.seq) * p.N + col);
                         float y[8], h[8], gg[8], z[8];
                         unpack8(v, y);
                         unpack8(hv, h);
@@ -586,6 +624,24 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
                     st_out(EPI == EPI_QKV_VT, reinterpret_cast<uint16_t *>(p.out) + grow * p.ldo + col, o);
                 }
             }
+        }
+        };
+        // Two versions only where pass 2 loads (gated residual, QK): the
+        // epilogues without loads wait for nothing there, and a second copy of
+        // their loop only lengthens live ranges across the main loop.
+        const bool all_rows = row0 + half * 64 + 64 <= p.M;  // uniform
+        if constexpr (EPI == QIM_EPI_GATED_RESIDUAL) {
+            if (all_rows && gate_once)
+                pass2(std::true_type{}, std::true_type{});
+            else
+                pass2(std::false_type{}, std::false_type{});
+        } else if constexpr (is_qk_epi<EPI>()) {
+            if (all_rows)
+                pass2(std::true_type{}, std::false_type{});
+            else
+                pass2(std::false_type{}, std::false_type{});
+        } else {
+            pass2(std::false_type{}, std::false_type{});
         }
     }
     }
