@@ -91,7 +91,7 @@ __global__ __launch_bounds__(64 * W) void k_quant_tile(Source src, uint8_t *__re
     Source in = src;
     in.start(row0 + rb, col);
 
-    // Loads in flight per lane: two rows at a time (all eight at once crowds
+    // Loads in flight per lane: two or four rows (all eight at once crowds
     // the L1 miss queue: measured slower).
     uint4 a[8], b[8];
     // Code offsets: row-major (row0 + r) * K + col; tiled (mxt_offset) the
@@ -102,17 +102,29 @@ __global__ __launch_bounds__(64 * W) void k_quant_tile(Source src, uint8_t *__re
     const int64_t n = Mp - r0 < 256 ? Mp - r0 : 256;
     const int64_t out0 = tiled ? r0 * K + (col >> 6) * n * 64 + (col & 15) : (row0 + rb) * K + col;
     const int rl = (int)(row0 + rb - r0), chunk = (int)((col >> 4) & 3);
+    // Rows two at a time; the next pair's loads are issued after this pair's
+    // arithmetic and before its stores, so that waiting for them never means
+    // waiting for stores (the vector-memory counter drains in issue order and
+    // counts stores too).
+    in.load(row0 + rb < M, 0, a[0], b[0]);
+    in.load(row0 + rb + 4 < M, 1, a[1], b[1]);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        if ((i & 1) == 0) {
-            in.load(row0 + rb + 4 * i < M, i, a[i], b[i]);
-            in.load(row0 + rb + 4 * i + 4 < M, i + 1, a[i + 1], b[i + 1]);
+    for (int i = 0; i < 8; i += 2) {
+        int e[2];
+        uint2 c[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) c[u] = in.quantize(a[i + u], b[i + u], e[u]);
+        if (i + 2 < 8) {
+            in.load(row0 + rb + 4 * (i + 2) < M, i + 2, a[i + 2], b[i + 2]);
+            in.load(row0 + rb + 4 * (i + 3) < M, i + 3, a[i + 3], b[i + 3]);
         }
-        int e;
-        const uint2 c = in.quantize(a[i], b[i], e);
-        const int rr = rl + 4 * i;
-        st_nt(q + out0 + (tiled ? (int64_t)(rr * 64 + ((chunk ^ mx_chunk_swizzle(rr)) << 4)) : i * 4 * K), c);
-        if ((c16 & 3) == 0) sb[(rsub + 4 * i) * 4 + (c16 >> 2)] = (uint8_t)e;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int rr = rl + 4 * (i + u);
+            st_nt(q + out0 + (tiled ? (int64_t)(rr * 64 + ((chunk ^ mx_chunk_swizzle(rr)) << 4)) : (i + u) * 4 * K),
+                  c[u]);
+            if ((c16 & 3) == 0) sb[(rsub + 4 * (i + u)) * 4 + (c16 >> 2)] = (uint8_t)e[u];
+        }
     }
     __syncthreads();
     // The tile's 512 scale bytes: row r (of 128) at (r % 32) * 16 + (r / 32) * 4;
