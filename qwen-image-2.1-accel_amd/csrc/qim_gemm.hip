@@ -419,18 +419,22 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
         [[maybe_unused]] bool gate_once = false;
         if constexpr (EPI == QIM_EPI_GATED_RESIDUAL) {
             const int cl = lane % LPR, gl = lane / LPR;
+            // Row h0 + lr, clamped to M - 1: a uniform base row hc and
+            // min(lr, M - 1 - hc) rows past it (32-bit per row).
+            const int64_t h0 = row0 + half * 64, hc = h0 < p.M ? h0 : p.M - 1;
+            const uint16_t *rb = p.res + hc * p.N;
+            const uint32_t lmax = (uint32_t)(p.M - 1 - hc), rcol = (uint32_t)(col0 + cl * 8);
 #pragma unroll
             for (int it = 0; it < 16 / GPI; ++it)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    int64_t grow = row0 + half * 64 + 4 * (it * GPI + gl) + r;
-                    grow = grow < p.M ? grow : p.M - 1;
-                    rpre[it][r] = ld_nt(p.res + grow * p.N + col0 + cl * 8);
+                    const uint32_t lr = (uint32_t)(4 * (it * GPI + gl) + r);
+                    rpre[it][r] = ld_nt(rb + ((lr < lmax ? lr : lmax) * (uint32_t)p.N + rcol));
                 }
-            const int64_t h0 = row0 + half * 64, h1 = (h0 + 63 < p.M ? h0 + 63 : p.M - 1);
-            const int64_t b0 = (h0 < p.M ? h0 : p.M - 1) / p.seq;
-            gate_once = b0 == h1 / p.seq;
-            gpre = *reinterpret_cast<const uint4 *>(p.gate + b0 * p.N + col0 + cl * 8);
+            const int64_t h1 = h0 + 63 < p.M ? h0 + 63 : p.M - 1;
+            const uint32_t b0 = (uint32_t)hc / (uint32_t)p.seq;
+            gate_once = b0 == (uint32_t)h1 / (uint32_t)p.seq;
+            gpre = *reinterpret_cast<const uint4 *>(p.gate + (int64_t)b0 * p.N + col0 + cl * 8);
         }
         // pass 1
 #pragma unroll
@@ -535,6 +539,41 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
                 load_freqs(0, fr[0]);
             }
         }
+        // MXFP8 output: the half's 64 rows lie in one 256-row group of the
+        // tiled layout and one 128-row block of the scales, so each row's
+        // code and scale offsets are a uniform base plus a per-lane 32-bit
+        // offset plus a compile-time row term (times a uniform row step for
+        // the codes): no 64-bit arithmetic per row.  Local row
+        // lr = 4 (it GPI + gl) + r; with GPI % 4 == 0 its chunk swizzle
+        // ((lr >> 1) ^ (lr >> 2)) & 3 is ((2 gl + r / 2) ^ gl) & 3.  Mp is a
+        // multiple of 128, so a half is stored whole or not at all.
+        // bf16 output rows: the same split, row h0 + lr at obase + ooff + lr * ldo.
+        [[maybe_unused]] uint16_t *const obase = reinterpret_cast<uint16_t *>(p.out) + (row0 + half * 64) * p.ldo;
+        [[maybe_unused]] const uint32_t ooff = (uint32_t)(col + 4 * gl * p.ldo);
+        [[maybe_unused]] uint8_t *qbase = nullptr, *sbase = nullptr;
+        [[maybe_unused]] uint32_t qoff[2] = {0, 0}, soff = 0, qstep = 0;
+        [[maybe_unused]] bool qlive = false;
+        if constexpr (EPI == QIM_EPI_SWIGLU_QUANT) {
+            static_assert(GPI % 8 == 0, "row terms below assume whole groups of 8 row groups");
+            const int64_t h0 = row0 + half * 64, kb = col >> 5;
+            qlive = h0 < p.Mp;
+            sbase = p.out_scales + (h0 >> 7) * (F >> 7) * 512 + ((h0 & 127) >> 5) * 4;
+            soff = (uint32_t)((kb >> 2) * 512 + (kb & 3) + (gl & 7) * 64 + (gl >> 3) * 4);
+            if (p.out_tiled) {
+                const int64_t r0 = h0 & ~int64_t(255);
+                const int64_t n = p.Mp - r0 < 256 ? p.Mp - r0 : 256;
+                qbase = reinterpret_cast<uint8_t *>(p.out) + r0 * F + (h0 - r0) * 64;
+                qstep = 64;
+                const uint32_t lo = (uint32_t)((col >> 6) * n * 64 + (col & 15) + gl * 4 * 64);
+                const int ch = (int)(col >> 4) & 3;
+#pragma unroll
+                for (int hb = 0; hb < 2; ++hb) qoff[hb] = lo + ((ch ^ (((2 * gl + hb) ^ gl) & 3)) << 4);
+            } else {
+                qbase = reinterpret_cast<uint8_t *>(p.out) + h0 * F;
+                qstep = (uint32_t)F;
+                qoff[0] = qoff[1] = (uint32_t)(col + gl * 4 * F);
+            }
+        }
         auto pass2 = [&](auto all_rows, auto one_gate) {
             constexpr bool ALL_ROWS = decltype(all_rows)::value, ONE_GATE = decltype(one_gate)::value;
 #pragma unroll
@@ -601,11 +640,8 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
                 if constexpr (EPI == QIM_EPI_SWIGLU_QUANT) {
                     int e;
                     const uint2 c = quantize8_bf16(v, e);
-                    if (grow < p.Mp) {
-                        const int64_t o = p.out_tiled ? mxt_offset(grow, col, p.Mp, F) : grow * F + col;
-                        st_nt(reinterpret_cast<uint8_t *>(p.out) + o, c);
-                        if ((cl & 3) == 0) p.out_scales[mx_scale_offset(grow, col >> 5, F)] = (uint8_t)e;
-                    }
+                    st_nt(qbase + (qoff[r >> 1] + (uint32_t)(4 * it * GPI + r) * qstep), c);
+                    if ((cl & 3) == 0) sbase[soff + (uint32_t)(16 * r + it * (GPI / 8) * 4)] = (uint8_t)e;
                 } else {
                     if (!ALL_ROWS && grow >= p.M) continue;
                     uint4 o = v;
@@ -621,7 +657,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
                         for (int t = 0; t < 8; ++t) z[t] = h[t] + rbf(gg[t] * y[t]);
                         o = pack8(z);
                     }
-                    st_out(EPI == EPI_QKV_VT, reinterpret_cast<uint16_t *>(p.out) + grow * p.ldo + col, o);
+                    st_out(EPI == EPI_QKV_VT, obase + (ooff + (uint32_t)(4 * it * GPI + r) * (uint32_t)p.ldo), o);
                 }
             }
         }
@@ -640,6 +676,8 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
                 pass2(std::true_type{}, std::false_type{});
             else
                 pass2(std::false_type{}, std::false_type{});
+        } else if constexpr (EPI == QIM_EPI_SWIGLU_QUANT) {
+            if (qlive) pass2(std::false_type{}, std::false_type{});
         } else {
             pass2(std::false_type{}, std::false_type{});
         }
@@ -893,6 +931,8 @@ static int gemm_run(const void *aq, const void *as, const void *bq, const void *
                 QIM_ERR_LAYOUT, "qim_mxfp8_gemm: operands must be 16-byte aligned");
     QIM_REQUIRE(epilogue == QIM_EPI_SWIGLU_QUANT || ldo % 8 == 0, QIM_ERR_LAYOUT,
                 "qim_mxfp8_gemm: ldo=%lld is not a multiple of 8", (long long)ldo);
+    // The epilogues address a 64-row half's outputs with 32-bit offsets.
+    QIM_REQUIRE(ldo < (1ll << 25), QIM_ERR_LAYOUT, "qim_mxfp8_gemm: ldo=%lld too large", (long long)ldo);
     QIM_REQUIRE(Mp / 128 < (1ll << 30), QIM_ERR_SHAPE, "qim_mxfp8_gemm: M=%lld too large", (long long)M);
     QIM_REQUIRE(Mp * K < (1ll << 31) && N * K < (1ll << 31), QIM_ERR_SHAPE,
                 "qim_mxfp8_gemm: operands above 2 GiB are not supported");
