@@ -342,6 +342,57 @@ __device__ __forceinline__ void tile_of(const GemmArgs &p, int &tm, int &tn) {
     tile_coords(p, t, tm, tn);
 }
 
+// ------------------------------------------------------------ SiLU table --
+// The SwiGLU epilogues look bf16(silu(g)) up instead of computing it (the
+// estimate, its band test and the rounding cost ~14 vector instructions per
+// output, on one wave per SIMD with nothing to hide them).  The table holds
+// every bf16 g with biased exponent 101..132 (2^-26 <= |g| < 128): entry i of
+// a sign is g = bits 0x3280 + i, positive at byte 2i, negative at 8192 + 2i,
+// so for the packed bf16 pair G the two byte addresses come from
+// P = G - 0x3280 (per half) as (P << 1) for bits 0..12 and (P >> 2) for the
+// sign at bit 13; a value is in the table when bits 12..14 of P are clear.
+// Entries are computed with silu_bf16 (bit-identical to the reference's
+// rounding) by each workgroup while its first stages' loads are in flight;
+// the rest (|g| < 2^-26, |g| >= 128, NaN) takes silu_bf16 itself.
+constexpr int SILU_TAB_BYTES = 16384;
+constexpr uint16_t SILU_TAB_BASE = 0x3280;
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+
+template <int EPI>
+constexpr int ring_offset() { return (EPI == QIM_EPI_SWIGLU || EPI == QIM_EPI_SWIGLU_QUANT) ? SILU_TAB_BYTES : 0; }
+
+__device__ __forceinline__ void fill_silu_table(uint8_t *tab) {
+    // 256 threads x 16 dwords (two entries each), dword d = c * 256 + t.
+#pragma unroll
+    for (int c0 = 0; c0 < 16; c0 += 4) {
+        float g[8], y[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t e = 2 * ((c0 + j / 2) * 256 + threadIdx.x) + (j & 1);  // entry 0..8191
+            const uint32_t b = SILU_TAB_BASE + (e & 4095) + ((e >> 12) << 15);
+            g[j] = __uint_as_float(b << 16);
+        }
+        silu_bf16_n<8>(g, y);
+#pragma unroll
+        for (int j = 0; j < 8; j += 2)
+            *reinterpret_cast<uint32_t *>(tab + 4 * ((c0 + j / 2) * 256 + threadIdx.x)) = pack_bf16x2(y[j], y[j + 1]);
+    }
+}
+
+// bf16(silu(g)) for the two bf16 values of gp (low half first), from the
+// table, as bf16 bits; `bad` collects the bits that mark a value outside it.
+__device__ __forceinline__ void silu_lookup2(const uint8_t *tab, uint32_t gp, uint32_t &y0, uint32_t &y1,
+                                             uint32_t &bad) {
+    const u16x2_t P = __builtin_bit_cast(u16x2_t, gp) - (u16x2_t){SILU_TAB_BASE, SILU_TAB_BASE};
+    bad |= __builtin_bit_cast(uint32_t, P) & 0x70007000u;
+    const uint32_t a = __builtin_bit_cast(uint32_t, (u16x2_t)(P << (u16x2_t){1, 1}));
+    const uint32_t b = __builtin_bit_cast(uint32_t, (u16x2_t)(P >> (u16x2_t){2, 2}));
+    uint32_t w;  // bits 0..12 of each half from a, bit 13 (and the zero bits above it) from b
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(w) : "s"(0x1fff1fffu), "v"(a), "v"(b));
+    y0 = *reinterpret_cast<const uint16_t *>(tab + (w & 0xffffu));
+    y1 = *reinterpret_cast<const uint16_t *>(tab + (w >> 16));
+}
+
 // ------------------------------------------------------------- epilogue --
 // Two passes per 64 rows (two MFMA row tiles) of the wave's block, through a
 // wave-private LDS region (the ring is free once the main loop has drained):
@@ -365,8 +416,9 @@ template <int W>
 __device__ __forceinline__ int epi_col_offset(int c) { return c * 8 + (c >> 3) * 16; }
 
 template <int EPI, int TI, int TJ>
-__device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][TJ], uint8_t *lds, int64_t row0,
-                                         int64_t gcol0, int lane, int wave) {
+__device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][TJ], uint8_t *lds,
+                                         [[maybe_unused]] const uint8_t *tab, int64_t row0, int64_t gcol0, int lane,
+                                         int wave) {
     if constexpr (EPI == EPI_F32 || EPI == EPI_F16) {
         // Straight from the accumulators: for each register, 32 lanes store
         // 32 consecutive columns of one row (128 or 64 contiguous bytes).
@@ -437,35 +489,79 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
             gpre = *reinterpret_cast<const uint4 *>(p.gate + (int64_t)b0 * p.N + col0 + cl * 8);
         }
         // pass 1
+        if constexpr (SWI) {
+            // bf16(bf16(silu(g)) * v) for the half's 8 row groups: g and v
+            // rounded to bf16 in pairs, every table read of the half issued
+            // before the first is used (their latency overlaps the rest), one
+            // rarely taken branch for values outside the table (recomputed
+            // from the accumulators), then the products; the store's bf16
+            // packing is the final rounding.
+            constexpr int NP = TJ;  // pairs per row group: TJ / 2 column pairs x 2 row pairs
+            uint32_t up[2][4][NP], bad = 0;
+            uint32_t y[2][4][2 * NP];  // bf16 bits
+#pragma unroll
+            for (int tl = 0; tl < 2; ++tl)
+#pragma unroll
+                for (int ig = 0; ig < 4; ++ig)
+#pragma unroll
+                    for (int u = 0; u < TJ / 2; ++u)
+#pragma unroll
+                        for (int e = 0; e < 4; e += 2) {
+                            const int ti = half * 2 + tl, k = 2 * u + e / 2;
+                            const uint32_t gp = pack_bf16x2(acc[ti][2 * u][4 * ig + e], acc[ti][2 * u][4 * ig + e + 1]);
+                            up[tl][ig][k] =
+                                pack_bf16x2(acc[ti][2 * u + 1][4 * ig + e], acc[ti][2 * u + 1][4 * ig + e + 1]);
+                            silu_lookup2(tab, gp, y[tl][ig][2 * k], y[tl][ig][2 * k + 1], bad);
+                        }
+            // Keep the conversions below from being scheduled up against
+            // their reads.
+            __builtin_amdgcn_sched_barrier(0);
+            if (__builtin_expect(bad != 0, 0)) {
+#pragma unroll
+                for (int tl = 0; tl < 2; ++tl)
+#pragma unroll
+                    for (int ig = 0; ig < 4; ++ig)
+#pragma unroll
+                        for (int u = 0; u < TJ / 2; ++u)
+#pragma unroll
+                            for (int e = 0; e < 4; e += 2) {
+                                const int ti = half * 2 + tl, k = 2 * u + e / 2;
+                                const uint32_t gp =
+                                    pack_bf16x2(acc[ti][2 * u][4 * ig + e], acc[ti][2 * u][4 * ig + e + 1]);
+#pragma unroll
+                                for (int h = 0; h < 2; ++h) {
+                                    const uint32_t gb = (gp >> (16 * h)) & 0xffffu;
+                                    if (((gb - SILU_TAB_BASE) & 0x7000u) != 0)
+                                        y[tl][ig][2 * k + h] = __float_as_uint(silu_bf16(__uint_as_float(gb << 16))) >> 16;
+                                }
+                            }
+            }
+#pragma unroll
+            for (int tl = 0; tl < 2; ++tl)
+#pragma unroll
+                for (int ig = 0; ig < 4; ++ig) {
+                    uint8_t *grp = reg + (tl * 8 + ig * 2 + kh) * RGS;  // rows 32tl + 8ig + 4kh + 0..3
+                    float yy[2 * NP];
+#pragma unroll
+                    for (int i = 0; i < 2 * NP; ++i) yy[i] = __uint_as_float(y[tl][ig][i] << 16);
+#pragma unroll
+                    for (int u = 0; u < TJ / 2; ++u) {
+                        const uint32_t v0 = up[tl][ig][2 * u], v1 = up[tl][ig][2 * u + 1];
+                        *reinterpret_cast<uint2 *>(grp + epi_col_offset<W>(u * 32 + lr)) =
+                            make_uint2(pack_bf16x2(yy[4 * u] * __uint_as_float(v0 << 16),
+                                                   yy[4 * u + 1] * __uint_as_float(v0 & 0xffff0000u)),
+                                       pack_bf16x2(yy[4 * u + 2] * __uint_as_float(v1 << 16),
+                                                   yy[4 * u + 3] * __uint_as_float(v1 & 0xffff0000u)));
+                    }
+                }
+        } else
 #pragma unroll
         for (int tl = 0; tl < 2; ++tl) {
             const int ti = half * 2 + tl;
 #pragma unroll
             for (int ig = 0; ig < 4; ++ig) {
                 uint8_t *grp = reg + (tl * 8 + ig * 2 + kh) * RGS;  // rows 32tl + 8ig + 4kh + 0..3
-                if constexpr (SWI) {
-                    // bf16(bf16(silu(g)) * v) on TJ / 2 x 4 values with one
-                    // exact-path branch; the store's bf16 packing is the final rounding.
-                    constexpr int NS = TJ / 2 * 4;
-                    float gs[NS], us[NS], y[NS];
-#pragma unroll
-                    for (int u = 0; u < TJ / 2; ++u)
-#pragma unroll
-                        for (int e = 0; e < 4; e += 2) {
-                            gs[4 * u + e] = acc[ti][2 * u][4 * ig + e];
-                            gs[4 * u + e + 1] = acc[ti][2 * u][4 * ig + e + 1];
-                            us[4 * u + e] = acc[ti][2 * u + 1][4 * ig + e];
-                            us[4 * u + e + 1] = acc[ti][2 * u + 1][4 * ig + e + 1];
-                            rbf2(gs[4 * u + e], gs[4 * u + e + 1]);
-                            rbf2(us[4 * u + e], us[4 * u + e + 1]);
-                        }
-                    silu_bf16_n<NS>(gs, y);
-#pragma unroll
-                    for (int u = 0; u < TJ / 2; ++u)
-                        *reinterpret_cast<uint2 *>(grp + epi_col_offset<W>(u * 32 + lr)) =
-                            make_uint2(pack_bf16x2(y[4 * u] * us[4 * u], y[4 * u + 1] * us[4 * u + 1]),
-                                       pack_bf16x2(y[4 * u + 2] * us[4 * u + 2], y[4 * u + 3] * us[4 * u + 3]));
-                } else if (vtw) {
+                if (vtw) {
 #pragma unroll
                     for (int tj = 0; tj < TJ; ++tj)
                         *reinterpret_cast<uint2 *>(reg + (tj * 32 + lr) * VT_COL + (32 * tl + 8 * ig + 4 * kh) * 2) =
@@ -791,7 +887,7 @@ __device__ __forceinline__ void qstep(const GemmArgs &p, const QPlan &Q, uint8_t
 }
 
 template <int EPI>
-__device__ __forceinline__ void quarter_tile(const GemmArgs &p, uint8_t *lds, int q) {
+__device__ __forceinline__ void quarter_tile(const GemmArgs &p, uint8_t *lds, uint8_t *tab, int q) {
     int64_t m0, n0;
     if (q < p.quarters) {  // a quarter of one of the last whole tiles
         const int tile = p.main_tiles + q / 4, quarter = q & 3;
@@ -817,6 +913,7 @@ __device__ __forceinline__ void quarter_tile(const GemmArgs &p, uint8_t *lds, in
     issue_qstage<false>(p, Q, lds + STAGE_BYTES, 1 < S ? 1 : S - 1);
     issue_qstage<true>(p, Q, lds + 2 * STAGE_BYTES, 2 < S ? 2 : S - 1);
     issue_qstage<false>(p, Q, lds + 3 * STAGE_BYTES, 3 < S ? 3 : S - 1);
+    if constexpr (ring_offset<EPI>() > 0) fill_silu_table(tab);
     wait_vmcnt<QLOADS_ODD + QLOADS_EVEN + QLOADS_ODD>();  // stage 0 landed
     block_barrier();
     QFrags fa, fb;
@@ -828,14 +925,17 @@ __device__ __forceinline__ void quarter_tile(const GemmArgs &p, uint8_t *lds, in
     wait_vmcnt<0>();
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     block_barrier();
-    epilogue<EPI, 2, 2>(p, acc, lds, m0 + wm * 64, n0 + wn * 64, lane, wave);
+    epilogue<EPI, 2, 2>(p, acc, lds, tab, m0 + wm * 64, n0 + wn * 64, lane, wave);
 }
 
 template <int EPI>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_mx_gemm(GemmArgs p) {
-    extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
+    extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+    // The SwiGLU kernels keep their SiLU table in the first 16 KiB; the ring
+    // (and the epilogue's staging) follows it.
+    uint8_t *const tab = smem, *const lds = smem + ring_offset<EPI>();
     if ((int)blockIdx.x >= p.main_tiles) {  // a quarter tile of the last partial round
-        quarter_tile<EPI>(p, lds, (int)blockIdx.x - p.main_tiles);
+        quarter_tile<EPI>(p, lds, tab, (int)blockIdx.x - p.main_tiles);
         return;
     }
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -857,6 +957,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     issue_stage<false>(p, L, lds + STAGE_BYTES, 1 < S ? 1 : S - 1);
     issue_stage<true>(p, L, lds + 2 * STAGE_BYTES, 2 < S ? 2 : S - 1);
     issue_stage<false>(p, L, lds + 3 * STAGE_BYTES, 3 < S ? 3 : S - 1);
+    if constexpr (ring_offset<EPI>() > 0) fill_silu_table(tab);
     wait_vmcnt<LOADS_ODD + LOADS_EVEN + LOADS_ODD>();  // stage 0 landed
     block_barrier();
     Frags fa, fb;
@@ -871,7 +972,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     block_barrier();
 
-    epilogue<EPI, 4, 4>(p, acc, lds, m0 + wm * 128, n0 + wn * 128, lane, wave);
+    epilogue<EPI, 4, 4>(p, acc, lds, tab, m0 + wm * 128, n0 + wn * 128, lane, wave);
 }
 
 // Whole tiles to launch: all of them, or all but the last r when the last
@@ -886,12 +987,13 @@ static int64_t main_tile_count(int64_t tiles) {
 template <int EPI>
 static int launch_gemm(const GemmArgs &a, hipStream_t st) {
     static std::atomic<bool> configured[QIM_MAX_DEVICES] = {};
-    if (const int rc = reserve_lds(reinterpret_cast<const void *>(&k_mx_gemm<EPI>), LDS_BYTES, configured,
+    constexpr int lds_bytes = LDS_BYTES + ring_offset<EPI>();
+    if (const int rc = reserve_lds(reinterpret_cast<const void *>(&k_mx_gemm<EPI>), lds_bytes, configured,
                                    "qim_mxfp8_gemm"))
         return rc;
     const int64_t half_column = a.tiles_n * BN < a.N ? (a.Mp + 127) / 128 : 0;
     const int64_t grid = a.main_tiles + a.quarters + half_column;
-    launch(k_mx_gemm<EPI>, dim3((unsigned)grid), dim3(256), LDS_BYTES, st, a);
+    launch(k_mx_gemm<EPI>, dim3((unsigned)grid), dim3(256), lds_bytes, st, a);
     return QIM_OK;
 }
 
