@@ -94,6 +94,17 @@ int qim_adaln_quantize(const void *x, const void *scale, const void *shift, cons
 int qim_gated_residual(const void *h, const void *x, const void *gate, void *out,
                        int64_t rows, int64_t D, int64_t seq, void *stream);
 
+/* The per-step modulation terms -- src/qwen_image_accel/optimizations/
+ * fusion.py:48-53 (1 + s1, tanh(g1), 1 + s2, tanh(g2) of the modulation
+ * chunks, computed there as eager torch ops): mod is (G, period, D) bf16 --
+ * G groups of `period` (1..16) rows -- and row i of each group is copied
+ * (kind 0), mapped to bf16(1 + x) (kind 1) or to bf16(tanh(x)) (kind 2: tanh
+ * in float64, rounded to fp32, then to bf16), kind = (kinds >> (2 * i)) & 3.
+ * out is (period, G, D): each term one contiguous block.  rows = G * period;
+ * D % 8 == 0. */
+int qim_modulation_values(const void *mod, int64_t rows, int64_t D, uint32_t kinds, int period,
+                          void *out, void *stream);
+
 /* swiglu(gate, value) -- src/qwen_image_accel/kernels/bf16.py:27-36 (kernel
  * :12-24): out = bf16(bf16(silu(g)) * v).  g, v, out: (M, F) with row strides
  * ldg, ldv, ldo (strided halves of one (M, 2F) tensor are accepted).

@@ -49,9 +49,54 @@ __global__ __launch_bounds__(256) void k_swiglu(const uint16_t *__restrict__ g, 
     st_nt(out + row * ldo + c * 8, pack8(o));
 }
 
+// The per-step modulation terms (reference optimizations/fusion.py:48-53:
+// 1 + s and tanh(g) of the modulation chunks, as bf16 tensors): rows of D
+// values, row r = g P + i (term i of group g) copied (kind 0), mapped to
+// bf16(1 + x) (kind 1) or to bf16(tanh(x)) (kind 2: tanh in float64, rounded
+// to fp32 and then to bf16); kind = (kinds >> 2 i) & 3.  Written term-major,
+// to row i G + g of out (G groups), so that each term is one contiguous block.
+__global__ __launch_bounds__(256) void k_modulation_values(const uint16_t *__restrict__ mod,
+                                                            uint16_t *__restrict__ out, uint32_t nvec,
+                                                            uint32_t d8, uint32_t kinds, uint32_t period,
+                                                            uint32_t groups) {
+    const uint32_t v = blockIdx.x * 256u + threadIdx.x;
+    if (v >= nvec) return;
+    const uint32_t r = v / d8, c = v - r * d8, grp = r / period, term = r - grp * period;
+    const uint32_t kind = (kinds >> (2u * term)) & 3u;
+    uint4 u = reinterpret_cast<const uint4 *>(mod)[v];
+    if (kind != 0) {
+        float f[8];
+        unpack8(u, f);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) f[i] = kind == 1 ? f[i] + 1.0f : (float)tanh((double)f[i]);
+        u = pack8(f);
+    }
+    reinterpret_cast<uint4 *>(out)[(term * groups + grp) * d8 + c] = u;
+}
+
 }  // namespace qim
 
 using namespace qim;
+
+extern "C" int qim_modulation_values(const void *mod, int64_t rows, int64_t D, uint32_t kinds, int period,
+                                     void *out, void *stream) {
+    QIM_REQUIRE(mod && out, QIM_ERR_ARG, "qim_modulation_values: null pointer");
+    QIM_REQUIRE(rows > 0 && D > 0, QIM_ERR_SHAPE, "qim_modulation_values: empty input");
+    QIM_REQUIRE(D % 8 == 0, QIM_ERR_SHAPE, "qim_modulation_values: D=%lld is not a multiple of 8", (long long)D);
+    QIM_REQUIRE(period >= 1 && period <= 16, QIM_ERR_ARG, "qim_modulation_values: period %d not in [1, 16]",
+                period);
+    for (int r = 0; r < period; ++r)
+        QIM_REQUIRE(((kinds >> (2 * r)) & 3u) != 3u, QIM_ERR_ARG, "qim_modulation_values: kind 3 for row %d", r);
+    QIM_REQUIRE(rows % period == 0, QIM_ERR_SHAPE, "qim_modulation_values: rows=%lld not a multiple of %d",
+                (long long)rows, period);
+    QIM_REQUIRE(rows * (D / 8) < (1ll << 31), QIM_ERR_SHAPE, "qim_modulation_values: too large");
+    QIM_REQUIRE(aligned16(mod) && aligned16(out), QIM_ERR_LAYOUT,
+                "qim_modulation_values: operands must be 16-byte aligned");
+    const uint32_t nvec = (uint32_t)(rows * (D / 8));
+    launch(k_modulation_values, dim3((nvec + 255) / 256), dim3(256), 0, as_stream(stream), (const uint16_t *)mod,
+           (uint16_t *)out, nvec, (uint32_t)(D / 8), kinds, (uint32_t)period, (uint32_t)(rows / period));
+    return check_launch("qim_modulation_values");
+}
 
 extern "C" int qim_gated_residual(const void *h, const void *x, const void *gate, void *out, int64_t rows,
                                   int64_t D, int64_t seq, void *stream) {

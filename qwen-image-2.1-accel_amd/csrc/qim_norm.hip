@@ -86,7 +86,10 @@ __device__ __forceinline__ bool ln_variance(double s2, double mean_d, int D, dou
 // the optional-operand branches the statistics waited for the residual too;
 // here they wait for x alone, the chain for the column vectors, and only the
 // final add for the residual (the last loads).
-template <bool QUANT, int NV, bool FULL, bool RG, bool ALL = false>
+// PLAIN: the scale is used as given (no QIM_ADALN_ADD_ONE); the general form
+// adds -0 and rounds, which leaves a bf16 value unchanged, at 2.5 vector
+// instructions per element.
+template <bool QUANT, int NV, bool FULL, bool RG, bool ALL = false, bool PLAIN = false>
 __global__ __launch_bounds__(FULL ? 64 * ADALN_FULL_WAVES : 64 * ADALN_MAX_WAVES) void k_adaln(AdaLNArgs p) {
     __shared__ double red[3][FULL ? ADALN_FULL_WAVES : ADALN_MAX_WAVES];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -287,8 +290,12 @@ __global__ __launch_bounds__(FULL ? 64 * ADALN_FULL_WAVES : 64 * ADALN_MAX_WAVES
         for (int t = 0; t < 8; t += 2) {
             float a0 = (x[i][t] - mean) * rstd, a1 = (x[i][t + 1] - mean) * rstd;
             rbf2(a0, a1);                                             // t0
-            float m0 = sf[t] + scale_add, m1 = sf[t + 1] + scale_add;
-            rbf2(m0, m1);                                             // t1
+            float m0 = sf[t], m1 = sf[t + 1];
+            if constexpr (!PLAIN) {
+                m0 += scale_add;
+                m1 += scale_add;
+                rbf2(m0, m1);                                         // t1
+            }
             a0 *= m0;
             a1 *= m1;
             rbf2(a0, a1);                                             // t2
@@ -359,7 +366,10 @@ static int launch_adaln_rg(const AdaLNArgs &a, hipStream_t st) {
             return QIM_OK;
         }
         if (k % 3 == 0 && k / 3 <= ADALN_FULL_WAVES) {
-            launch((k_adaln<QUANT, 3, true, RG>), grid, dim3(64 * (k / 3)), 0, st, a);
+            if (QUANT && !RG && !(a.flags & QIM_ADALN_ADD_ONE))  // the block's quantizing AdaLN
+                launch((k_adaln<QUANT, 3, true, RG, false, true>), grid, dim3(64 * (k / 3)), 0, st, a);
+            else
+                launch((k_adaln<QUANT, 3, true, RG>), grid, dim3(64 * (k / 3)), 0, st, a);
             return QIM_OK;
         }
         if (k % 4 == 0 && k / 4 <= ADALN_FULL_WAVES) {

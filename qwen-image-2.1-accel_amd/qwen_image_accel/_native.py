@@ -41,6 +41,7 @@ _P = ctypes.c_void_p
 _I = ctypes.c_int64
 _F = ctypes.c_float
 _C = ctypes.c_int
+_U = ctypes.c_uint32
 
 SIGNATURES = {
     "qim_last_error": (ctypes.c_char_p, []),
@@ -50,6 +51,7 @@ SIGNATURES = {
     "qim_adaln": (_C, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _C, _P]),
     "qim_adaln_quantize": (_C, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _C, _P]),
     "qim_gated_residual": (_C, [_P, _P, _P, _P, _I, _I, _I, _P]),
+    "qim_modulation_values": (_C, [_P, _I, _I, _U, _C, _P, _P]),
     "qim_swiglu": (_C, [_P, _I, _P, _I, _P, _I, _I, _I, _P]),
     "qim_swiglu_quantize": (_C, [_P, _I, _P, _I, _P, _P, _I, _I, _P]),
     "qim_swiglu_quantize_tiled": (_C, [_P, _I, _P, _I, _P, _P, _I, _I, _P]),

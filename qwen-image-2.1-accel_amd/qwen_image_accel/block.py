@@ -18,20 +18,21 @@ modulation, fused QKV projection, hidden 3072, 24 heads x 128, FFN 12288):
     a   = MXFP8(silu(x @ W_gate) * (x @ W_up))              GEMM, SwiGLU->MXFP8 epilogue
     h   = h + tanh(g2) * (a @ W_down)                       GEMM, gated-residual epilogue
 
-Seven launches (QK-RMSNorm + RoPE run in the QKV GEMM's epilogue, head by
-head: each wave of the GEMM holds whole 128-wide head rows); every MXFP8 operand (weights and activations) is in the GEMM's
-tiled code layout, written that way by its producer; every bf16 rounding point
-of the eager block is kept (the
+Eight launches, all of this library: the modulation terms and the seven
+above (QK-RMSNorm + RoPE run in the QKV GEMM's epilogue, head by head: each
+wave of the GEMM holds whole 128-wide head rows); every MXFP8 operand (weights
+and activations) is in the GEMM's tiled code layout, written that way by its
+producer; every bf16 rounding point of the eager block is kept (the
 activation quantizations share one FP8 tensor per consumer group, as in
-quantized_decode.py:50-53, 81-96).  The modulation precompute (1 + s is done
-inside the LayerNorm kernel, tanh(g) in eager torch) is the reference's
-per-step precompute (optimizations/fusion.py:48-53).
+quantized_decode.py:50-53, 81-96).  The modulation precompute (1 + s and
+tanh(g) of the six modulation rows, one launch of qim_modulation_values) is
+the reference's per-step precompute (optimizations/fusion.py:48-53).
 """
 from dataclasses import dataclass
 
 import torch
 
-from qwen_image_accel.kernels import attention, gemm, mxfp8
+from qwen_image_accel.kernels import attention, elementwise, gemm, mxfp8
 from qwen_image_accel.kernels.epilogue import layer_norm_scale_quantize
 
 
@@ -45,6 +46,16 @@ class _LayerNorm:
 
     def __call__(self, x):
         return torch.nn.functional.layer_norm(x, self.normalized_shape, eps=self.eps)
+
+
+def modulation_terms(modulation):
+    """(shift1, 1 + scale1, tanh(gate1), shift2, 1 + scale2, tanh(gate2)), each
+    (B, 1, D) bf16, from the (B, 6, D) modulation rows in one launch
+    (qim_modulation_values): the reference's per-step precompute
+    (optimizations/fusion.py:48-53) in the MMDiT layout."""
+    k = elementwise
+    mv = k.modulation_values(modulation.contiguous(), (k.MOD_COPY, k.MOD_ONE_PLUS, k.MOD_TANH) * 2)
+    return tuple(mv[i].unsqueeze(1) for i in range(6))  # each (B, 1, D), contiguous
 
 
 @dataclass
@@ -101,16 +112,11 @@ class MMDiTBlock:
         receives the intermediate results (x1, qkv, o, h1, x2, a) for
         checking; nothing is copied."""
         b, s, d = h.shape
-        shift1, scale1, _, shift2, scale2, _ = (modulation[:, i:i + 1] for i in range(6))
-        # tanh of all six rows in one vectorised launch (2.2 us; the strided
-        # gate rows alone take the slower strided path, 3.7 us)
-        tanh_mod = modulation.tanh()
-        gate1, gate2 = tanh_mod[:, 2:3], tanh_mod[:, 5:6]
+        shift1, scale1, gate1, shift2, scale2, gate2 = modulation_terms(modulation)
         norm = _LayerNorm(d, self.eps)
         hd = d // self.heads
 
-        x = layer_norm_scale_quantize(h, scale1.contiguous(), norm, shift=shift1.contiguous(),
-                                      add_one=True, tiled=True)
+        x = layer_norm_scale_quantize(h, scale1, norm, shift=shift1, add_one=False, tiled=True)
         ws = None
         if fused_attention:
             if s % 64:
@@ -129,15 +135,14 @@ class MMDiTBlock:
         else:
             o = qkv[:, 2 * d:] if attention_fn is None else attention_fn(q, k, v).reshape(b * s, d)  # stand-in: v
             oq = mxfp8.quantize(o, tiled=True)
-        h1 = self._mm(oq, self.w_out, epilogue="gated_residual", gate=gate1.contiguous(),
+        h1 = self._mm(oq, self.w_out, epilogue="gated_residual", gate=gate1,
                       residual=h.reshape(b * s, d), seq=s)
         h1 = h1.view(b, s, d)
-        x2 = layer_norm_scale_quantize(h1, scale2.contiguous(), norm, shift=shift2.contiguous(),
-                                       add_one=True, tiled=True)
+        x2 = layer_norm_scale_quantize(h1, scale2, norm, shift=shift2, add_one=False, tiled=True)
         a = self._mm(x2, self.w_gate_up, epilogue="swiglu_quant", out_tiled=True)
         if stages is not None:
             stages.update(x1=x, qkv=qkv, o=oq, h1=h1, x2=x2, a=a)
-        h2 = self._mm(a, self.w_down, epilogue="gated_residual", gate=gate2.contiguous(),
+        h2 = self._mm(a, self.w_down, epilogue="gated_residual", gate=gate2,
                       residual=h1.reshape(b * s, d), seq=s)
         return h2.view(b, s, d)
 

@@ -28,6 +28,30 @@ def residual(h, x, gate):
     return h + gate * x
 
 
+MOD_COPY, MOD_ONE_PLUS, MOD_TANH = 0, 1, 2
+
+
+def modulation_values(mod, kinds):
+    """The per-step modulation terms (reference optimizations/fusion.py:48-53,
+    ``1 + s`` and ``tanh(g)`` of the modulation chunks) in one launch.
+
+    mod: (..., P, D) contiguous bf16 on the GPU; row i of each group of P rows
+    is copied (MOD_COPY), mapped to bf16(1 + x) (MOD_ONE_PLUS) or to
+    bf16(tanh(x)) (MOD_TANH; tanh in float64, rounded to fp32, then to bf16),
+    i.e. kinds[i].  Returns (P, ..., D): term i is the contiguous ``out[i]``."""
+    p, d = len(kinds), mod.shape[-1]
+    if not (mod.is_cuda and mod.dtype == torch.bfloat16 and mod.is_contiguous() and mod.ndim >= 2
+            and mod.shape[-2] == p and 1 <= p <= 16 and d % 8 == 0 and mod.numel() > 0
+            and all(k in (MOD_COPY, MOD_ONE_PLUS, MOD_TANH) for k in kinds)):
+        raise _native.Unsupported("modulation_values", _native.QIM_ERR_ARG,
+                                  f"{tuple(mod.shape)} {mod.dtype} kinds={kinds}")
+    out = torch.empty((p,) + tuple(mod.shape[:-2]) + (d,), dtype=mod.dtype, device=mod.device)
+    bits = sum(k << (2 * i) for i, k in enumerate(kinds))
+    _native.call("qim_modulation_values", _native.ptr(mod), mod.numel() // d, d, bits, p, _native.ptr(out),
+                 _native.stream(mod.device))
+    return out
+
+
 def rope_qk(q, k, freqs):
     """Complex RoPE of q and k (B, S, H, D) with freqs (S, D/2) complex64.
 

@@ -28,7 +28,8 @@ def unfused_block(blk, h, mod, freqs):
     b, s, d = h.shape
     hd = d // blk.heads
     shift1, scale1, g1, shift2, scale2, g2 = (mod[:, i:i + 1] for i in range(6))
-    gate1, gate2 = g1.tanh().contiguous(), g2.tanh().contiguous()
+    gate1 = elementwise.modulation_values(g1.contiguous(), (elementwise.MOD_TANH,))[0].unsqueeze(1)
+    gate2 = elementwise.modulation_values(g2.contiguous(), (elementwise.MOD_TANH,))[0].unsqueeze(1)
     norm = _LayerNorm(d, blk.eps)
 
     def mm(x, w):

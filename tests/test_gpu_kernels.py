@@ -12,6 +12,7 @@ import pytest
 import torch
 import torch.nn.functional as F
 
+from oracle import block as OB
 from oracle import oracle as O
 from qwen_image_accel import _native
 from qwen_image_accel.kernels import attention, bf16, elementwise, epilogue, gemm, layernorm, mxfp8
@@ -120,6 +121,27 @@ def test_scaled_mfma_lane_layout(dev):
     got = out.cpu().numpy()
     assert np.all(np.abs(got - ref) <= bound), np.max(np.abs(got - ref) / bound)
     assert rel_fro(got, ref) < 1e-3
+
+
+def test_modulation_values_exhaustive(dev):
+    """qim_modulation_values on every bf16 value: tanh rows equal the oracle's
+    tanh (float64 tanh, rounded to fp32, then to bf16), 1 + x rows equal torch's
+    bf16 addition on the CPU (fp32 sum rounded to nearest even), copied rows
+    are unchanged."""
+    allb = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16).reshape(64, 1024)
+    mod = torch.stack([allb, allb, allb], dim=1).contiguous()  # (64, 3, 1024)
+    kinds = (elementwise.MOD_COPY, elementwise.MOD_ONE_PLUS, elementwise.MOD_TANH)
+    out = elementwise.modulation_values(mod.to(dev), kinds).cpu()
+    assert out.shape == (3, 64, 1024)
+    got = {k: bits(out[i]).astype(np.int64) for i, k in enumerate(("copy", "one", "tanh"))}
+    want = {"copy": bits(allb).astype(np.int64), "one": bits(1 + allb).astype(np.int64),
+            "tanh": OB.tanh_bf16(bits(allb)).astype(np.int64)}
+    for k in got:
+        g, w = got[k], want[k]
+        nan_g = (g & 0x7f80 == 0x7f80) & (g & 0x7f != 0)
+        nan_w = (w & 0x7f80 == 0x7f80) & (w & 0x7f != 0)
+        assert np.array_equal(nan_g, nan_w), k
+        assert np.array_equal(g[~nan_g], w[~nan_w]), (k, int((g[~nan_g] != w[~nan_w]).sum()))
 
 
 def test_silu_exhaustive(dev):

@@ -47,6 +47,11 @@ def test_abi_version():
     ("qim_mx_quantize", (16, 128, 1, 100, 16, 16, None), _native.QIM_ERR_SHAPE),
     ("qim_mx_quantize", (17, 128, 1, 128, 16, 16, None), _native.QIM_ERR_LAYOUT),
     ("qim_gated_residual", (16, 16, 16, 16, 4, 12, 4, None), _native.QIM_ERR_SHAPE),
+    # modulation terms: a period of 0, a row of kind 3, D not a multiple of 8
+    ("qim_modulation_values", (16, 6, 16, 0, 0, 16, None), _native.QIM_ERR_ARG),
+    ("qim_modulation_values", (16, 6, 16, 0b110000, 3, 16, None), _native.QIM_ERR_ARG),
+    ("qim_modulation_values", (16, 6, 12, 0b100100, 3, 16, None), _native.QIM_ERR_SHAPE),
+    ("qim_modulation_values", (16, 7, 16, 0b100100, 3, 16, None), _native.QIM_ERR_SHAPE),
     ("qim_swiglu", (16, 8, 16, 8, 16, 4, 1, 8, None), _native.QIM_ERR_LAYOUT),
     ("qim_rms_norm", (16, 16, 16, 4, 96, 1e-6, None), _native.QIM_ERR_SHAPE),
     ("qim_adaln", (16, 16, None, None, None, 16, 1, 16392, 1, 1e-6, 0, None), _native.QIM_ERR_SHAPE),
