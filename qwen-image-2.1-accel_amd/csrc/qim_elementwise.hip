@@ -55,23 +55,22 @@ __global__ __launch_bounds__(256) void k_swiglu(const uint16_t *__restrict__ g, 
 // bf16(1 + x) (kind 1) or to bf16(tanh(x)) (kind 2: tanh in float64, rounded
 // to fp32 and then to bf16); kind = (kinds >> 2 i) & 3.  Written term-major,
 // to row i G + g of out (G groups), so that each term is one contiguous block.
+// One value per lane: the launch is a few thousand values, and its time is
+// one lane's float64 tanh.
 __global__ __launch_bounds__(256) void k_modulation_values(const uint16_t *__restrict__ mod,
-                                                            uint16_t *__restrict__ out, uint32_t nvec,
-                                                            uint32_t d8, uint32_t kinds, uint32_t period,
+                                                            uint16_t *__restrict__ out, uint32_t n,
+                                                            uint32_t d, uint32_t kinds, uint32_t period,
                                                             uint32_t groups) {
     const uint32_t v = blockIdx.x * 256u + threadIdx.x;
-    if (v >= nvec) return;
-    const uint32_t r = v / d8, c = v - r * d8, grp = r / period, term = r - grp * period;
+    if (v >= n) return;
+    const uint32_t r = v / d, c = v - r * d, grp = r / period, term = r - grp * period;
     const uint32_t kind = (kinds >> (2u * term)) & 3u;
-    uint4 u = reinterpret_cast<const uint4 *>(mod)[v];
+    uint16_t u = mod[v];
     if (kind != 0) {
-        float f[8];
-        unpack8(u, f);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) f[i] = kind == 1 ? f[i] + 1.0f : (float)tanh((double)f[i]);
-        u = pack8(f);
+        const float f = bf16_to_f32(u);
+        u = (uint16_t)pack_bf16x2(kind == 1 ? f + 1.0f : (float)tanh((double)f), 0.0f);
     }
-    reinterpret_cast<uint4 *>(out)[(term * groups + grp) * d8 + c] = u;
+    out[(term * groups + grp) * d + c] = u;
 }
 
 }  // namespace qim
@@ -89,12 +88,12 @@ extern "C" int qim_modulation_values(const void *mod, int64_t rows, int64_t D, u
         QIM_REQUIRE(((kinds >> (2 * r)) & 3u) != 3u, QIM_ERR_ARG, "qim_modulation_values: kind 3 for row %d", r);
     QIM_REQUIRE(rows % period == 0, QIM_ERR_SHAPE, "qim_modulation_values: rows=%lld not a multiple of %d",
                 (long long)rows, period);
-    QIM_REQUIRE(rows * (D / 8) < (1ll << 31), QIM_ERR_SHAPE, "qim_modulation_values: too large");
+    QIM_REQUIRE(rows * D < (1ll << 31), QIM_ERR_SHAPE, "qim_modulation_values: too large");
     QIM_REQUIRE(aligned16(mod) && aligned16(out), QIM_ERR_LAYOUT,
                 "qim_modulation_values: operands must be 16-byte aligned");
-    const uint32_t nvec = (uint32_t)(rows * (D / 8));
-    launch(k_modulation_values, dim3((nvec + 255) / 256), dim3(256), 0, as_stream(stream), (const uint16_t *)mod,
-           (uint16_t *)out, nvec, (uint32_t)(D / 8), kinds, (uint32_t)period, (uint32_t)(rows / period));
+    const uint32_t n = (uint32_t)(rows * D);
+    launch(k_modulation_values, dim3((n + 255) / 256), dim3(256), 0, as_stream(stream), (const uint16_t *)mod,
+           (uint16_t *)out, n, (uint32_t)D, kinds, (uint32_t)period, (uint32_t)(rows / period));
     return check_launch("qim_modulation_values");
 }
 
