@@ -28,14 +28,15 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
 }
 
 // Eager ".to(bfloat16)" boundary: the fp32 value of the bf16 rounding of x.
-__device__ __forceinline__ float rbf(float x) { return bf_lo(pack_bf16x2(x, 0.0f)); }
+// Converting the pair (0, x) puts bf16(x) in the high half above a zero low
+// half, which is that fp32 value: one v_cvt_pk_bf16_f32 and no unpacking.
+__device__ __forceinline__ float rbf(float x) { return __uint_as_float(pack_bf16x2(0.0f, x)); }
 
-// Round two values to bf16 in one conversion (v_cvt_pk_bf16_f32) and widen
-// them back: the same results as rbf(a), rbf(b).
+// Round two values to bf16: two such conversions (one conversion of the pair
+// and two unpacking operations would take three instructions).
 __device__ __forceinline__ void rbf2(float &a, float &b) {
-    const uint32_t u = pack_bf16x2(a, b);
-    a = bf_lo(u);
-    b = bf_hi(u);
+    a = rbf(a);
+    b = rbf(b);
 }
 
 // Unpack 8 bf16 (one 16-byte vector) to fp32.
