@@ -281,6 +281,12 @@ int qim_debug_mfma_probe(int shape, float *out, void *stream);
 /* bf16(silu(g)) of n bf16 values with the rounding every SwiGLU kernel uses
  * (reference kernels/bf16.py:17-22: bf16(g / (1 + exp(-g)))). */
 int qim_debug_silu(const void *g, void *out, int64_t n, void *stream);
+/* The normalisations' reciprocal square root (fp32(1 / sqrt(double(var + eps))),
+ * a fast path with an interval check and that expression as fallback) against
+ * its definition for var = the fp32 values with bit patterns [first, first +
+ * count): bad (2 uint32, the caller sets 0 and 0xffffffff) receives the number
+ * of disagreements and the smallest disagreeing pattern. */
+int qim_debug_rstd_sweep(uint32_t first, uint32_t count, float eps, void *bad, void *stream);
 /* Streaming device copy of nbytes (a multiple of 16, 16-byte aligned): the
  * bandwidth reference of the benchmarks and the calibration kernel of the HBM
  * byte counters.  No reference counterpart. */

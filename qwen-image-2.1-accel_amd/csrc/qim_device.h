@@ -261,21 +261,23 @@ __device__ __forceinline__ double wave_total(double v) {
 // statistics define it: t = var + eps in fp32, then R = fp32(1 / sqrt(t))
 // evaluated in float64 (IEEE sqrt and divide) and rounded once.
 //
-// Fast path with the same result: y = v_rsq_f32(t) (relative error < 2^-22)
-// refined by two float64 Newton steps (error < 2^-50 after the second), so
-// the exact 1/sqrt(t) and the float64 value of R both lie within
-// y (1 +- 2^-40).  When both ends of that interval round to the same fp32
-// value, so does everything inside it, R included; otherwise (a value within
-// 2^-40 of an fp32 rounding midpoint, or a non-finite or non-positive t,
-// where the Newton steps give NaN) the float64 expression is evaluated.
+// Fast path with the same result: y = v_rsq_f32(t) (relative error d < 2^-22)
+// refined by one float64 Newton step, after which the relative error is
+// 1.5 d^2 + O(2^-52) < 2^-42, so the exact 1/sqrt(t) and the float64 value of
+// R both lie within y (1 +- 2^-38) (the margin allows d up to 2^-19).  When
+// both ends of that interval round to the same fp32 value, so does everything
+// inside it, R included; otherwise (a value within 2^-38 of an fp32 rounding
+// midpoint, about one in 8000, a non-finite t, or a t that is not positive:
+// v_rsq_f32 takes a negative denormal for -0 and the step then gives -inf,
+// not NaN) the float64 expression is evaluated.  Checked against that
+// expression for all 2^32 fp32 values of var (qim_debug_rstd_sweep).
 __device__ __forceinline__ float rstd_of(float var, float eps) {
     const float t = var + eps;
     const double td = (double)t;
     double y = (double)__builtin_amdgcn_rsqf(t);
     y = __builtin_fma(y, __builtin_fma(-td * y, y, 1.0) * 0.5, y);
-    y = __builtin_fma(y, __builtin_fma(-td * y, y, 1.0) * 0.5, y);
-    const float lo = (float)(y * (1.0 - 0x1p-40)), hi = (float)(y * (1.0 + 0x1p-40));
-    if (__builtin_expect(lo == hi, 1)) return lo;
+    const float lo = (float)(y * (1.0 - 0x1p-38)), hi = (float)(y * (1.0 + 0x1p-38));
+    if (__builtin_expect(lo == hi && t > 0.0f, 1)) return lo;
     return (float)(1.0 / sqrt(td));
 }
 

@@ -173,6 +173,22 @@ __global__ void k_debug_silu(const uint16_t *__restrict__ g, uint16_t *__restric
     out[i] = (uint16_t)(__float_as_uint(y) >> 16);
 }
 
+// rstd_of(v, eps) against its definition fp32(1 / sqrt(double(v + eps)))
+// for the fp32 values v with bit patterns [first, first + count): bad[0]
+// counts disagreements, bad[1] keeps the smallest disagreeing pattern.
+__global__ void k_debug_rstd_sweep(uint32_t first, uint32_t count, float eps, uint32_t *bad) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= count) return;
+    const uint32_t bits = first + i;
+    const float v = __uint_as_float(bits);
+    const float fast = rstd_of(v, eps);
+    const float ref = (float)(1.0 / sqrt((double)(v + eps)));
+    if (__float_as_uint(fast) != __float_as_uint(ref)) {
+        atomicAdd(bad, 1u);
+        atomicMin(bad + 1, bits);
+    }
+}
+
 // Streaming copy, one 16-byte vector per lane: the achievable-bandwidth
 // reference and the calibration kernel of the HBM byte counters.
 __global__ __launch_bounds__(256) void k_debug_copy(const uint4 *__restrict__ src, uint4 *__restrict__ dst,
@@ -240,6 +256,17 @@ extern "C" int qim_debug_silu(const void *g, void *out, int64_t n, void *stream)
     launch(k_debug_silu, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, as_stream(stream),
                        (const uint16_t *)g, (uint16_t *)out, n);
     return check_launch("qim_debug_silu");
+}
+
+extern "C" int qim_debug_rstd_sweep(uint32_t first, uint32_t count, float eps, void *bad, void *stream) {
+    QIM_REQUIRE(bad, QIM_ERR_ARG, "qim_debug_rstd_sweep: null pointer");
+    QIM_REQUIRE((uint64_t)first + count <= 0x100000000ull, QIM_ERR_SHAPE,
+                "qim_debug_rstd_sweep: patterns past 2^32");
+    QIM_REQUIRE(((uintptr_t)bad & 3u) == 0, QIM_ERR_LAYOUT, "qim_debug_rstd_sweep: bad must be 4-byte aligned");
+    if (count == 0) return QIM_OK;
+    launch(k_debug_rstd_sweep, dim3((unsigned)(((uint64_t)count + 255) / 256)), dim3(256), 0, as_stream(stream),
+           first, count, eps, (uint32_t *)bad);
+    return check_launch("qim_debug_rstd_sweep");
 }
 
 extern "C" int qim_debug_copy(const void *src, void *dst, int64_t nbytes, void *stream) {

@@ -75,6 +75,7 @@ SIGNATURES = {
     "qim_debug_copy": (_C, [_P, _P, _I, _P]),
     "qim_debug_copy_ex": (_C, [_P, _P, _I, _C, _C, _P]),
     "qim_debug_silu": (_C, [_P, _P, _I, _P]),
+    "qim_debug_rstd_sweep": (_C, [_U, _U, _F, _P, _P]),
 }
 
 _lib = None

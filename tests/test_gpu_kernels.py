@@ -165,6 +165,22 @@ def test_silu_exhaustive(dev):
     assert np.all(np.isnan(bf16_values(got)[nan]))
 
 
+def test_rstd_exhaustive(dev):
+    """The normalisations' reciprocal square root (v_rsq_f32 refined in
+    float64, an interval check, the float64 expression as fallback) equals its
+    definition fp32(1 / sqrt(double(var + eps))) for every one of the 2^32 fp32
+    bit patterns of var (eps 0, so t = var + 0 runs over every fp32 value; and
+    eps 1e-6, the configs' value), so RMSNorm's and AdaLN's rstd is pinned for
+    all inputs.  The comparison runs on the device and counts disagreements."""
+    for eps in (0.0, 1e-6):
+        say("rstd exhaustive, eps", eps)
+        bad = torch.tensor([0, -1], dtype=torch.int32, device=dev)
+        for first in (0, 1 << 31):
+            _native.call("qim_debug_rstd_sweep", first, 1 << 31, eps, _native.ptr(bad), _native.stream())
+        n, low = (int(x) & 0xffffffff for x in bad.cpu().tolist())
+        assert n == 0, (eps, n, hex(low))
+
+
 def test_streaming_copy(dev):
     """The bandwidth/counter calibration copy and its ceiling variants move
     every byte, tails included, and nothing past the end."""

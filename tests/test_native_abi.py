@@ -52,6 +52,10 @@ def test_abi_version():
     ("qim_modulation_values", (16, 6, 16, 0b110000, 3, 16, None), _native.QIM_ERR_ARG),
     ("qim_modulation_values", (16, 6, 12, 0b100100, 3, 16, None), _native.QIM_ERR_SHAPE),
     ("qim_modulation_values", (16, 7, 16, 0b100100, 3, 16, None), _native.QIM_ERR_SHAPE),
+    # rstd sweep: no counter buffer; patterns past 2^32; a misaligned counter buffer
+    ("qim_debug_rstd_sweep", (0, 16, 0.0, None, None), _native.QIM_ERR_ARG),
+    ("qim_debug_rstd_sweep", (0xffffff00, 0x200, 0.0, 16, None), _native.QIM_ERR_SHAPE),
+    ("qim_debug_rstd_sweep", (0, 16, 0.0, 18, None), _native.QIM_ERR_LAYOUT),
     ("qim_swiglu", (16, 8, 16, 8, 16, 4, 1, 8, None), _native.QIM_ERR_LAYOUT),
     ("qim_rms_norm", (16, 16, 16, 4, 96, 1e-6, None), _native.QIM_ERR_SHAPE),
     ("qim_adaln", (16, 16, None, None, None, 16, 1, 16392, 1, 1e-6, 0, None), _native.QIM_ERR_SHAPE),
