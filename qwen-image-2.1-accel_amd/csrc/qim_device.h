@@ -191,6 +191,9 @@ __device__ __forceinline__ float dpp_mov(float v) {
     return __uint_as_float(dpp_mov<CTRL>(__float_as_uint(v)));
 }
 constexpr int DPP_QUAD_XOR1 = 0xB1, DPP_QUAD_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_ROW_MIRROR = 0x140;
+// row_shl:n -- lane l of a 16-lane row receives lane l + n of the same row
+// (lanes past the row's end are not meaningful).
+constexpr int DPP_ROW_SHL4 = 0x104, DPP_ROW_SHL8 = 0x108, DPP_ROW_SHL12 = 0x10C;
 
 // Reduction over groups of WIDTH consecutive lanes (WIDTH a power of two <= 64);
 // every lane of the group receives the total.  Widths up to 16 stay in DPP

@@ -267,6 +267,31 @@ __global__ __launch_bounds__(FULL ? 64 * ADALN_FULL_WAVES : 64 * ADALN_MAX_WAVES
     }
     const float mean = (float)mean_d;
     const float rstd = rstd_of(var, p.eps);
+    // Quantized output addressing.  The row is uniform, so vector i's code
+    // and scale offsets (mxt_offset or row-major, and mx_scale_offset, at
+    // k = 8 j, j = tid + nthr i) are a per-row base, a per-lane 32-bit term
+    // and i times a uniform step: nthr is a multiple of 64, so i moves the
+    // 64-byte K-slab by nthr / 8, keeps the chunk and byte inside it, and
+    // moves the scale dword (4 blocks of 32) by nthr / 16.
+    [[maybe_unused]] uint8_t *qrow = nullptr, *srow = nullptr;
+    [[maybe_unused]] uint32_t qlane = 0, qstep = 0, slane = 0, sstep = 0;
+    if constexpr (QUANT) {
+        if (p.tiled) {
+            const int64_t r0 = row & ~int64_t(255);
+            const uint32_t slab = (uint32_t)(p.rows_pad - r0 < 256 ? p.rows_pad - r0 : 256) * 64;
+            qrow = p.q + r0 * p.D + (row - r0) * 64;
+            qlane = (uint32_t)(tid >> 3) * slab + ((uint32_t)(((tid >> 1) & 3) ^ mx_chunk_swizzle(row)) << 4) +
+                    (uint32_t)(tid & 1) * 8;
+            qstep = (uint32_t)(nthr >> 3) * slab;
+        } else {
+            qrow = p.q + row * p.D;
+            qlane = (uint32_t)tid * 8;
+            qstep = (uint32_t)nthr * 8;
+        }
+        srow = p.qs + (row >> 7) * (p.D >> 7) * 512 + (row & 31) * 16 + ((row & 127) >> 5) * 4;
+        slane = (uint32_t)(tid >> 4) * 512;
+        sstep = (uint32_t)(nthr >> 4) * 512;
+    }
     // t1 = bf16(scale + 1) with add_one, else scale (+ -0 leaves it unchanged).
     const float scale_add = (p.flags & QIM_ADALN_ADD_ONE) ? 1.0f : -0.0f;
     if constexpr (LATE) load_scale_shift();
@@ -317,16 +342,17 @@ __global__ __launch_bounds__(FULL ? 64 * ADALN_FULL_WAVES : 64 * ADALN_MAX_WAVES
         } else {
             // A 32-element block is 4 adjacent lanes; 4 adjacent blocks (16
             // lanes) own one dword of the swizzled scale array.
+            // The exponents of lanes + 4, + 8, + 12 arrive by DPP row shifts
+            // (inside the lane's 16-lane row).
             int e;
             const uint2 c = quantize8_bf16(packed, e);
-            st_nt(p.q + adaln_code_offset(p, row, j), c);
-            const uint32_t e1 = (uint32_t)__shfl((int)e, lane + 4, 64);
-            const uint32_t e2 = (uint32_t)__shfl((int)e, lane + 8, 64);
-            const uint32_t e3 = (uint32_t)__shfl((int)e, lane + 12, 64);
+            st_nt(qrow + (qlane + (uint32_t)i * qstep), c);
+            const uint32_t e1 = dpp_mov<DPP_ROW_SHL4>((uint32_t)e);
+            const uint32_t e2 = dpp_mov<DPP_ROW_SHL8>((uint32_t)e);
+            const uint32_t e3 = dpp_mov<DPP_ROW_SHL12>((uint32_t)e);
             if ((lane & 15) == 0) {
-                const int64_t kb = (int64_t)j >> 2;  // block index of this lane, multiple of 4
                 const uint32_t word = (uint32_t)e | (e1 << 8) | (e2 << 16) | (e3 << 24);
-                *reinterpret_cast<uint32_t *>(p.qs + mx_scale_offset(row, kb, p.D)) = word;
+                *reinterpret_cast<uint32_t *>(srow + (slane + (uint32_t)i * sstep)) = word;
             }
         }
     }
