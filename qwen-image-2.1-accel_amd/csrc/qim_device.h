@@ -302,6 +302,19 @@ __device__ __forceinline__ double head_sumsq8(const float *x) {
 }
 // x: the chunk; ss: the row's total sum of squares over `width` values; w: the
 // chunk's 8 weights.  Roundings are paired (one v_cvt_pk_bf16_f32 per two).
+// head_rmsnorm8 with the row's reciprocal square root r already computed.
+__device__ __forceinline__ void head_rmsnorm8_r(float *x, float r, const float *w) {
+#pragma unroll
+    for (int t = 0; t < 8; t += 2) {
+        float a = x[t] * r, b = x[t + 1] * r;
+        rbf2(a, b);
+        a *= w[t];
+        b *= w[t + 1];
+        rbf2(a, b);
+        x[t] = a;
+        x[t + 1] = b;
+    }
+}
 __device__ __forceinline__ void head_rmsnorm8(float *x, double ss, int width, float eps, const float *w) {
     const float r = rstd_of((float)(ss / (double)width), eps);
 #pragma unroll

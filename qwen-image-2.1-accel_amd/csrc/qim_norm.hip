@@ -438,29 +438,47 @@ struct NormRopeArgs {
     int64_t main_blocks; // workgroups of the norm/rope part; the rest copy the prefix
 };
 
-// Head rows per lane of one wave: a wave owns U * (64 / (D / 8)) heads of one
-// tensor of one token (8 at D = 128 with U = 2).  Measured on MI355X at
-// config 2 (steady-state clocks, rotating buffers): U = 2 19.4 us, U = 3
-// 19.6 us, U = 1 24-26 us, U = 6 (a whole tensor of a token per wave) 21.0 us;
-// a copy-only kernel of the same shape 19.3-19.7 us, so the arithmetic is
-// hidden.  The launch picks U in {2, 3, 4} so that the heads divide into whole
-// waves and no lane tests its head index; other head counts take the masked
-// kernel with U = 3.
+// Head rows per lane of one wave: with V 16-byte vectors of a row per lane, a
+// row is D / (8 V) lanes and a wave owns U * (64 / (D / (8 V))) heads of one
+// tensor of one token.  Measured on MI355X at config 2 (steady-state clocks,
+// rotating buffers), V = 1: U = 2 19.4 us, U = 3 19.6 us, U = 1 24-26 us,
+// U = 6 (a whole tensor of a token per wave) 21.0 us; a copy-only kernel of
+// the same shape 19.3-19.7 us.  The kernel is bound by its vector ALU as much
+// as by HBM (~250 vector instructions per wave, ~70 % of its time at
+// 4 cycles each), and the per-row work (the float64 row-sum reduction and the
+// reciprocal square root) is repeated by every lane of a row, so the launch
+// prefers V = 2 (half as many lanes per row, each row's work done once per
+// 16 values instead of 8) when the heads divide into whole waves; the other
+// splits keep V = 1 and pick U in {2, 3, 4} so that no lane tests its head
+// index; other head counts take the masked kernel with U = 3.
 constexpr int NR_ROWS = 3;
 
-// Normalise (optionally) and rotate (optionally) one 8-value chunk of a head
-// row; LPR lanes share the row (the helpers are in qim_device.h).
-template <int LPR, bool NORM, bool ROPE>
-__device__ __forceinline__ uint4 norm_rope_chunk(const uint4 &xv, const float *w, float eps, const float4 &f0,
-                                                 const float4 &f1) {
-    float x[8];
-    unpack8(xv, x);
+// Normalise (optionally) and rotate (optionally) the V 8-value chunks a lane
+// holds of one head row (chunks c and c + LPR, ... of the row: each 16-byte
+// load instruction of the wave covers whole 8 * LPR-value row segments); LPR
+// lanes share the row (the helpers are in qim_device.h).
+template <int LPR, int V, bool NORM, bool ROPE>
+__device__ __forceinline__ void norm_rope_chunks(const uint4 (&xv)[V], uint4 (&out)[V], const float (&w)[V][8],
+                                                 float eps, const float4 (&f0)[V], const float4 (&f1)[V]) {
+    float x[V][8];
+#pragma unroll
+    for (int v = 0; v < V; ++v) unpack8(xv[v], x[v]);
     if constexpr (NORM) {
-        const double ss = group_sum<LPR>(head_sumsq8(x));
-        head_rmsnorm8(x, ss, LPR * 8, eps, w);
+        // The float64 sum of the squares of bf16 values is exact, so adding
+        // the chunks' sums first leaves it unchanged.
+        double ss = head_sumsq8(x[0]);
+#pragma unroll
+        for (int v = 1; v < V; ++v) ss += head_sumsq8(x[v]);
+        ss = group_sum<LPR>(ss);
+        const float r = rstd_of((float)(ss / (double)(LPR * 8 * V)), eps);
+#pragma unroll
+        for (int v = 0; v < V; ++v) head_rmsnorm8_r(x[v], r, w[v]);
     }
-    if constexpr (ROPE) head_rope8(x, f0, f1);
-    return pack8(x);
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+        if constexpr (ROPE) head_rope8(x[v], f0[v], f1[v]);
+        out[v] = pack8(x[v]);
+    }
 }
 
 // q/k: (B, S, H, D) -> oq (B, S, H, D), ok (B, P+S, H, D); v -> ov at the
@@ -469,14 +487,15 @@ __device__ __forceinline__ uint4 norm_rope_chunk(const uint4 &xv, const float *w
 //
 // Wave w of the main part owns head group w % groups of tensor
 // (w / groups) % NTENS (0 = q, 1 = k, 2 = v) of token w / (NTENS * groups):
-// NR_ROWS head rows per lane, LPR lanes per row, all loads issued before any
-// arithmetic.  Neighbouring waves share a token, so its RoPE row is read from
-// HBM once and from L2 by the others.  Head slots past H are skipped (uniform
-// over the LPR lanes of a row).  v is copied unchanged.
-template <int D, bool NORM, bool ROPE, int NTENS, int U, bool FULL>
+// U head rows per lane, LPR lanes per row, V vectors per lane per row, all
+// loads issued before any arithmetic.  Neighbouring waves share a token, so
+// its RoPE row is read from HBM once and from L2 by the others.  Head slots
+// past H are skipped (uniform over the LPR lanes of a row).  v is copied
+// unchanged.
+template <int D, bool NORM, bool ROPE, int NTENS, int U, bool FULL, int V>
 __global__ __launch_bounds__(256) void k_norm_rope(NormRopeArgs p) {
-    constexpr int LPR = D / 8;       // lanes per head row
-    constexpr int RPI = 64 / LPR;    // head rows per wave instruction
+    constexpr int LPR = D / (8 * V);  // lanes per head row
+    constexpr int RPI = 64 / LPR;     // head rows per wave instruction
     const int lane = threadIdx.x & 63;
     const int g = lane / LPR, c = lane % LPR;
     if ((int64_t)blockIdx.x < p.main_blocks) {
@@ -501,65 +520,89 @@ __global__ __launch_bounds__(256) void k_norm_rope(NormRopeArgs p) {
             const int64_t kv_row = ((int64_t)bb * (p.P + p.S) + p.P + tok) * H + hb;
             dst = (tensor == 1 ? p.ok : p.ov) + kv_row * D;
         }
-        const int off = g * D + c * 8;  // this lane's elements within the item
-        uint4 x[U];
+        const int off = g * D + c * 8;  // this lane's first vector within the item; vector v at + 8 LPR v
+        uint4 x[U][V];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int h = h0 + u * RPI;
-            if (FULL || h < H) x[u] = ld_nt(src + off + u * RPI * D);
+            if (FULL || h < H) {
+#pragma unroll
+                for (int v = 0; v < V; ++v) x[u][v] = ld_nt(src + off + u * RPI * D + v * 8 * LPR);
+            }
         }
         if (NTENS == 3 && tensor == 2) {
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const int h = h0 + u * RPI;
-                if (FULL || h < H) st_nt(dst + off + u * RPI * D, x[u]);
+                if (FULL || h < H) {
+#pragma unroll
+                    for (int v = 0; v < V; ++v) st_nt(dst + off + u * RPI * D + v * 8 * LPR, x[u][v]);
+                }
             }
             return;
         }
-        float4 f0 = make_float4(0.f, 0.f, 0.f, 0.f), f1 = f0;
-        if constexpr (ROPE) {
-            const float4 *fr = reinterpret_cast<const float4 *>(p.freqs + (int64_t)tok * D + c * 8);
-            f0 = fr[0];
-            f1 = fr[1];
+        float4 f0[V], f1[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+            f0[v] = make_float4(0.f, 0.f, 0.f, 0.f);
+            f1[v] = f0[v];
+            if constexpr (ROPE) {
+                const float4 *fr = reinterpret_cast<const float4 *>(p.freqs + (int64_t)tok * D + (c + v * LPR) * 8);
+                f0[v] = fr[0];
+                f1[v] = fr[1];
+            }
         }
-        float wt[8];
-        if constexpr (NORM) unpack8(*reinterpret_cast<const uint4 *>((tensor == 0 ? p.wq : p.wk) + c * 8), wt);
+        float wt[V][8];
+        if constexpr (NORM) {
+#pragma unroll
+            for (int v = 0; v < V; ++v)
+                unpack8(*reinterpret_cast<const uint4 *>((tensor == 0 ? p.wq : p.wk) + (c + v * LPR) * 8), wt[v]);
+        }
         const float eps = tensor == 0 ? p.epsq : p.epsk;
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int h = h0 + u * RPI;
-            if (FULL || h < H) st_nt(dst + off + u * RPI * D, norm_rope_chunk<LPR, NORM, ROPE>(x[u], wt, eps, f0, f1));
+            if (FULL || h < H) {
+                uint4 o[V];
+                norm_rope_chunks<LPR, V, NORM, ROPE>(x[u], o, wt, eps, f0, f1);
+#pragma unroll
+                for (int v = 0; v < V; ++v) st_nt(dst + off + u * RPI * D + v * 8 * LPR, o[v]);
+            }
         }
     } else if constexpr (NTENS == 3) {
-        // Prefix copy: B * P * H rows of D, RPI rows per wave instruction.
+        // Prefix copy: B * P * H rows of D, D / 8 lanes per row.
+        constexpr int LPC = D / 8;
+        const int cc = lane % LPC;
         const int64_t gi = ((int64_t)blockIdx.x - p.main_blocks) * 256 + threadIdx.x;
-        const int64_t row = gi / LPR;
+        const int64_t row = gi / LPC;
         const int64_t PH = p.P * p.H;
         const int64_t B = p.T / p.S;
         if (row >= B * PH) return;
         const int64_t bb = row / PH, within = row - bb * PH;
-        const int64_t dst = (bb * (p.P + p.S) * p.H + within) * D + c * 8;
-        *reinterpret_cast<uint4 *>(p.ok + dst) = *reinterpret_cast<const uint4 *>(p.ck + row * D + c * 8);
-        *reinterpret_cast<uint4 *>(p.ov + dst) = *reinterpret_cast<const uint4 *>(p.cv + row * D + c * 8);
+        const int64_t dst = (bb * (p.P + p.S) * p.H + within) * D + cc * 8;
+        *reinterpret_cast<uint4 *>(p.ok + dst) = *reinterpret_cast<const uint4 *>(p.ck + row * D + cc * 8);
+        *reinterpret_cast<uint4 *>(p.ov + dst) = *reinterpret_cast<const uint4 *>(p.cv + row * D + cc * 8);
     }
 }
 
-template <int D, bool NORM, bool ROPE, int NTENS, int U, bool FULL>
+template <int D, bool NORM, bool ROPE, int NTENS, int U, bool FULL, int V = 1>
 static void launch_norm_rope_shape(NormRopeArgs a, int64_t prefix_blocks, hipStream_t st) {
-    const int64_t rows_per_wave = U * (512 / D);
+    const int64_t rows_per_wave = U * (512 * V / D);
     const int64_t groups = (a.H + rows_per_wave - 1) / rows_per_wave;
     const int64_t waves = a.T * NTENS * groups;
     a.groups = (uint32_t)groups;
     a.main_waves = (uint32_t)waves;
     a.main_blocks = (waves + 3) / 4;
-    launch((k_norm_rope<D, NORM, ROPE, NTENS, U, FULL>), dim3((unsigned)(a.main_blocks + prefix_blocks)),
+    launch((k_norm_rope<D, NORM, ROPE, NTENS, U, FULL, V>), dim3((unsigned)(a.main_blocks + prefix_blocks)),
                        dim3(256), 0, st, a);
 }
 
 template <int D, bool NORM, bool ROPE, int NTENS>
 static void launch_norm_rope_d(const NormRopeArgs &a, int64_t prefix_blocks, hipStream_t st) {
     constexpr int64_t RPI = 512 / D;
-    if (a.H % (2 * RPI) == 0) launch_norm_rope_shape<D, NORM, ROPE, NTENS, 2, true>(a, prefix_blocks, st);
+    if (D >= 128 && a.H % (2 * RPI) == 0)
+        launch_norm_rope_shape<D, NORM, ROPE, NTENS, 1, true, 2>(a, prefix_blocks, st);
+    else if (a.H % (2 * RPI) == 0) launch_norm_rope_shape<D, NORM, ROPE, NTENS, 2, true>(a, prefix_blocks, st);
     else if (a.H % (3 * RPI) == 0) launch_norm_rope_shape<D, NORM, ROPE, NTENS, 3, true>(a, prefix_blocks, st);
     else if (a.H % (4 * RPI) == 0) launch_norm_rope_shape<D, NORM, ROPE, NTENS, 4, true>(a, prefix_blocks, st);
     else launch_norm_rope_shape<D, NORM, ROPE, NTENS, NR_ROWS, false>(a, prefix_blocks, st);
