@@ -2,12 +2,16 @@
 //
 // The unit of work is a 128-row x 128-column tile, the unit of the
 // reference's scale layout: its 512 E8M0 bytes form one contiguous chunk of
-// the swizzled scale array.  A wave owns 32 rows of a tile; 16 lanes cover
-// one 128-column row (8 bf16 = one 16-byte load per lane), 4 rows per pass,
-// 8 passes, loads two passes at a time.  A 32-element block is 4 adjacent
+// the swizzled scale array, row r's 4 exponents at (r % 32) * 16 + (r / 32) * 4.
+// A wave owns 32 rows of a tile: rows 8w .. 8w + 7 of each 32-row quarter
+// (w = the wave's role), so its 32 exponent dwords are 8 whole 16-byte groups,
+// one contiguous 128-byte store.  (Owning 32 consecutive rows made each wave
+// write one dword of every 16 bytes of the chunk: 4 partial writes per 32-byte
+// sector, 1.2 MB of extra HBM writes at config 4a.)  16 lanes cover one
+// 128-column row (8 bf16 = one 16-byte load per lane), 4 rows per pass, 8
+// passes, loads two passes at a time.  A 32-element block is 4 adjacent
 // lanes, reduced with two DPP quad permutes; the codes come from the packed
-// bf16 values through the scaled conversion (no unpacking, no multiply).  A
-// wave's 32 x 4 exponents are staged in LDS and written one dword per row.
+// bf16 values through the scaled conversion (no unpacking, no multiply).
 // Workgroups are one wave (a quarter tile; measured fastest at config 4a).
 // HBM traffic is the algorithmic minimum: every input byte read once, every
 // code and scale byte written once.  Codes are written row-major or in the
@@ -21,15 +25,17 @@ namespace qim {
 struct QuantSource {
     const uint16_t *x;
     int64_t ldx;
-    // Loads of rows row + 4i (i = 0..7) at column col: pointer and step set once.
+    // Loads of rows row + pass_row(i) (i = 0..7) at column col: pointer and
+    // the two row steps set once.
     const uint16_t *px;
-    int64_t step;
+    int64_t s4, s32;
     __device__ __forceinline__ void start(int64_t row, int64_t col) {
         px = x + row * ldx + col;
-        step = 4 * ldx;
+        s4 = 4 * ldx;
+        s32 = 32 * ldx;
     }
     __device__ __forceinline__ void load(bool live, int i, uint4 &a, uint4 &b) const {
-        a = live ? ld_nt(px + i * step) : make_uint4(0, 0, 0, 0);
+        a = live ? ld_nt(px + (i >> 1) * s32 + (i & 1) * s4) : make_uint4(0, 0, 0, 0);
         (void)b;
     }
     // The 8 bf16 values as they are: converted packed, no unpacking.
@@ -48,16 +54,18 @@ struct SwigluSource {
     const uint16_t *v;
     int64_t ldv;
     const uint16_t *pg, *pv;
-    int64_t sg, sv;
+    int64_t sg4, sg32, sv4, sv32;
     __device__ __forceinline__ void start(int64_t row, int64_t col) {
         pg = g + row * ldg + col;
         pv = v + row * ldv + col;
-        sg = 4 * ldg;
-        sv = 4 * ldv;
+        sg4 = 4 * ldg;
+        sg32 = 32 * ldg;
+        sv4 = 4 * ldv;
+        sv32 = 32 * ldv;
     }
     __device__ __forceinline__ void load(bool live, int i, uint4 &a, uint4 &b) const {
-        a = live ? ld_nt(pg + i * sg) : make_uint4(0, 0, 0, 0);
-        b = live ? ld_nt(pv + i * sv) : make_uint4(0, 0, 0, 0);
+        a = live ? ld_nt(pg + (i >> 1) * sg32 + (i & 1) * sg4) : make_uint4(0, 0, 0, 0);
+        b = live ? ld_nt(pv + (i >> 1) * sv32 + (i & 1) * sv4) : make_uint4(0, 0, 0, 0);
     }
     __device__ __forceinline__ uint2 quantize(const uint4 &a, const uint4 &b, int &e) const {
         float gg[8], vv[8], s[8], f[8];
@@ -73,11 +81,20 @@ struct SwigluSource {
 // W waves per workgroup.  W = 4: one workgroup per 128 x 128 tile; W = 1:
 // one per 32-row quarter of it (wave role = blockIdx.x % 4), so a launch has
 // four times as many workgroups and the last round of the CUs is fuller.
+// Row of pass i (0..7) relative to the lane's base row 8w + rsub: passes
+// 2q and 2q + 1 cover rows 8w .. 8w + 7 of quarter q.
+__device__ __forceinline__ int pass_row(int i) { return 32 * (i >> 1) + 4 * (i & 1); }
+
+// W waves per workgroup.  W = 4: one workgroup per 128 x 128 tile; W = 1:
+// one per quarter of its rows (wave role = blockIdx.x % 4), so a launch has
+// four times as many workgroups and the last round of the CUs is fuller.
 template <class Source, int W>
 __global__ __launch_bounds__(64 * W) void k_quant_tile(Source src, uint8_t *__restrict__ q,
                                                         uint8_t *__restrict__ scales, int64_t M,
                                                         int64_t K, int tiled) {
-    __shared__ uint32_t s_scale[W][32];  // per wave: row r % 32 -> its 4 exponent bytes
+    // Per wave: its 32 exponent dwords in the order of the scale chunk, row
+    // j (0..7 of the 8w + j rows) of quarter q at dword j * 4 + q.
+    __shared__ uint32_t s_scale[W][32];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = W == 1 ? (int)(blockIdx.x & 3) : tid >> 6;
     const int c16 = lane & 15;    // 8-column chunk of the 128-column tile row
@@ -85,9 +102,9 @@ __global__ __launch_bounds__(64 * W) void k_quant_tile(Source src, uint8_t *__re
     const int64_t row0 = (int64_t)(W == 1 ? blockIdx.x >> 2 : blockIdx.x) * 128;
     const int64_t col = (int64_t)blockIdx.y * 128 + c16 * 8;
     uint8_t *sb = reinterpret_cast<uint8_t *>(s_scale[W == 1 ? 0 : wave]);
-    // This lane's rows are rb + 4i (i = 0..7) of the tile; their addresses
-    // advance by a fixed step, computed once.
-    const int rb = wave * 32 + rsub;
+    // This lane's rows are rb + pass_row(i) (i = 0..7) of the tile; their
+    // addresses advance by fixed steps, computed once.
+    const int rb = wave * 8 + rsub;
     Source in = src;
     in.start(row0 + rb, col);
 
@@ -96,9 +113,9 @@ __global__ __launch_bounds__(64 * W) void k_quant_tile(Source src, uint8_t *__re
     uint4 a[8], b[8];
     // Code offsets: row-major (row0 + r) * K + col; tiled (mxt_offset) the
     // 256-row super-block's slab of col plus 64 bytes per row and the row's
-    // chunk swizzle -- the lane's 8 rows share the super-block.
+    // chunk swizzle -- the tile's 128 rows share the super-block.
     const int64_t Mp = (int64_t)gridDim.x * (W == 1 ? 32 : 128);
-    const int64_t r0 = (row0 + rb) & ~int64_t(255);
+    const int64_t r0 = row0 & ~int64_t(255);
     const int64_t n = Mp - r0 < 256 ? Mp - r0 : 256;
     const int64_t out0 = tiled ? r0 * K + (col >> 6) * n * 64 + (col & 15) : (row0 + rb) * K + col;
     const int rl = (int)(row0 + rb - r0), chunk = (int)((col >> 4) & 3);
@@ -106,8 +123,8 @@ __global__ __launch_bounds__(64 * W) void k_quant_tile(Source src, uint8_t *__re
     // arithmetic and before its stores, so that waiting for them never means
     // waiting for stores (the vector-memory counter drains in issue order and
     // counts stores too).
-    in.load(row0 + rb < M, 0, a[0], b[0]);
-    in.load(row0 + rb + 4 < M, 1, a[1], b[1]);
+    in.load(row0 + rb + pass_row(0) < M, 0, a[0], b[0]);
+    in.load(row0 + rb + pass_row(1) < M, 1, a[1], b[1]);
 #pragma unroll
     for (int i = 0; i < 8; i += 2) {
         int e[2];
@@ -115,27 +132,25 @@ __global__ __launch_bounds__(64 * W) void k_quant_tile(Source src, uint8_t *__re
 #pragma unroll
         for (int u = 0; u < 2; ++u) c[u] = in.quantize(a[i + u], b[i + u], e[u]);
         if (i + 2 < 8) {
-            in.load(row0 + rb + 4 * (i + 2) < M, i + 2, a[i + 2], b[i + 2]);
-            in.load(row0 + rb + 4 * (i + 3) < M, i + 3, a[i + 3], b[i + 3]);
+            in.load(row0 + rb + pass_row(i + 2) < M, i + 2, a[i + 2], b[i + 2]);
+            in.load(row0 + rb + pass_row(i + 3) < M, i + 3, a[i + 3], b[i + 3]);
         }
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            const int rr = rl + 4 * (i + u);
-            st_nt(q + out0 + (tiled ? (int64_t)(rr * 64 + ((chunk ^ mx_chunk_swizzle(rr)) << 4)) : (i + u) * 4 * K),
+            const int rr = rl + pass_row(i + u);
+            st_nt(q + out0 + (tiled ? (int64_t)(rr * 64 + ((chunk ^ mx_chunk_swizzle(rr)) << 4))
+                                    : (int64_t)pass_row(i + u) * K),
                   c[u]);
-            if ((c16 & 3) == 0) sb[(rsub + 4 * (i + u)) * 4 + (c16 >> 2)] = (uint8_t)e[u];
+            // Row j = 4 * ((i + u) & 1) + rsub of quarter (i + u) >> 1.
+            if ((c16 & 3) == 0) sb[(4 * ((i + u) & 1) + rsub) * 16 + ((i + u) >> 1) * 4 + (c16 >> 2)] = (uint8_t)e[u];
         }
     }
     __syncthreads();
-    // The tile's 512 scale bytes: row r (of 128) at (r % 32) * 16 + (r / 32) * 4;
-    // each wave's 32 rows are one dword per 16 bytes.
-    uint8_t *chunk0 = scales + ((int64_t)(row0 >> 7) * (K >> 7) + blockIdx.y) * 512;
-    if (W == 1) {
-        if (lane < 32) *reinterpret_cast<uint32_t *>(chunk0 + lane * 16 + wave * 4) = s_scale[0][lane];
-    } else if (tid < 32) {
-        *reinterpret_cast<uint4 *>(chunk0 + tid * 16) =
-            make_uint4(s_scale[0][tid], s_scale[W > 1 ? 1 : 0][tid], s_scale[W > 2 ? 2 : 0][tid], s_scale[W > 3 ? 3 : 0][tid]);
-    }
+    // This wave's 128 contiguous bytes of the tile's 512-byte scale chunk:
+    // rows 8w .. 8w + 7 of every quarter.
+    uint8_t *chunk0 = scales + ((int64_t)(row0 >> 7) * (K >> 7) + blockIdx.y) * 512 + wave * 128;
+    if (lane < 8)
+        *reinterpret_cast<uint4 *>(chunk0 + lane * 16) = reinterpret_cast<const uint4 *>(sb)[lane];
 }
 
 // Workgroups of one wave (W = 1) or four (W = 4): the launch shape of the
