@@ -448,6 +448,15 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
     const int lr = lane & 31, kh = lane >> 5;
     uint8_t *reg = lds + wave * (16 * RGS);
     const int64_t col0 = SWI ? gcol0 / 2 : gcol0;  // first output column
+    // SwiGLU -> MXFP8 in a whole tile (TI = 4): the two waves of a 128-row
+    // block (wave & 1 = 0, 1) together produce its 512-byte scale chunk (128
+    // rows x the tile's 4 blocks of 32 output columns).  Their exponent bytes
+    // are staged in LDS, after every wave's staging region, and the chunk
+    // leaves as 32 whole 16-byte stores: byte stores straight to memory wrote
+    // each 64-byte segment of the scales in many partial writes (+45 % of the
+    // kernel's HBM writes at 4352 x 24576 x 3072).
+    constexpr bool STAGE_SC = EPI == QIM_EPI_SWIGLU_QUANT && TI == 4;
+    [[maybe_unused]] uint8_t *const sc_stage = lds + 4 * 16 * RGS + (wave >> 1) * 512;
     const int64_t F = p.N / 2;
     // QKV projection with vt: this wave's V columns are staged per column (64
     // keys, VT_COL bytes apart; the odd stride spreads the pass-1 writes of a
@@ -647,7 +656,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
         [[maybe_unused]] uint16_t *const obase = reinterpret_cast<uint16_t *>(p.out) + (row0 + half * 64) * p.ldo;
         [[maybe_unused]] const uint32_t ooff = (uint32_t)(col + 4 * gl * p.ldo);
         [[maybe_unused]] uint8_t *qbase = nullptr, *sbase = nullptr;
-        [[maybe_unused]] uint32_t qoff[2] = {0, 0}, soff = 0, qstep = 0;
+        [[maybe_unused]] uint32_t qoff[2] = {0, 0}, soff = 0, sst = 0, qstep = 0;
         [[maybe_unused]] bool qlive = false;
         if constexpr (EPI == QIM_EPI_SWIGLU_QUANT) {
             static_assert(GPI % 8 == 0, "row terms below assume whole groups of 8 row groups");
@@ -655,6 +664,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
             qlive = h0 < p.Mp;
             sbase = p.out_scales + (h0 >> 7) * (F >> 7) * 512 + ((h0 & 127) >> 5) * 4;
             soff = (uint32_t)((kb >> 2) * 512 + (kb & 3) + (gl & 7) * 64 + (gl >> 3) * 4);
+            sst = (uint32_t)((kb & 3) + (gl & 7) * 64 + (gl >> 3) * 4 + ((h0 & 127) >> 5) * 4);
             if (p.out_tiled) {
                 const int64_t r0 = h0 & ~int64_t(255);
                 const int64_t n = p.Mp - r0 < 256 ? p.Mp - r0 : 256;
@@ -737,7 +747,12 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
                     int e;
                     const uint2 c = quantize8_bf16(v, e);
                     st_nt(qbase + (qoff[r >> 1] + (uint32_t)(4 * it * GPI + r) * qstep), c);
-                    if ((cl & 3) == 0) sbase[soff + (uint32_t)(16 * r + it * (GPI / 8) * 4)] = (uint8_t)e;
+                    if ((cl & 3) == 0) {
+                        if constexpr (STAGE_SC)
+                            sc_stage[sst + (uint32_t)(16 * r + it * (GPI / 8) * 4)] = (uint8_t)e;
+                        else
+                            sbase[soff + (uint32_t)(16 * r + it * (GPI / 8) * 4)] = (uint8_t)e;
+                    }
                 } else {
                     if (!ALL_ROWS && grow >= p.M) continue;
                     uint4 o = v;
@@ -776,6 +791,15 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
             if (qlive) pass2(std::false_type{}, std::false_type{});
         } else {
             pass2(std::false_type{}, std::false_type{});
+        }
+    }
+    if constexpr (STAGE_SC) {
+        // Both halves of both waves of each 128-row block staged (a block
+        // below Mp is live in both halves: Mp % 128 == 0).
+        __syncthreads();
+        if ((wave & 1) == 0 && lane < 32 && row0 < p.Mp) {
+            uint8_t *chunk = p.out_scales + ((row0 >> 7) * (F >> 7) + (col0 >> 7)) * 512;
+            *reinterpret_cast<uint4 *>(chunk + lane * 16) = *reinterpret_cast<const uint4 *>(sc_stage + lane * 16);
         }
     }
     }
