@@ -746,7 +746,12 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f32x16_t (&acc)[TI][
                 if constexpr (EPI == QIM_EPI_SWIGLU_QUANT) {
                     int e;
                     const uint2 c = quantize8_bf16(v, e);
-                    st_nt(qbase + (qoff[r >> 1] + (uint32_t)(4 * it * GPI + r) * qstep), c);
+                    // Cached, not streaming: a store instruction covers half of
+                    // each 128-byte line (rows 4 apart), and streamed half-line
+                    // writes reached memory as 1.5x the code bytes (WRITE_SIZE
+                    // 78207 vs 53952 KiB at 4352 x 24576 x 3072); through the
+                    // cache the two halves merge.
+                    *reinterpret_cast<uint2 *>(qbase + (qoff[r >> 1] + (uint32_t)(4 * it * GPI + r) * qstep)) = c;
                     if ((cl & 3) == 0) {
                         if constexpr (STAGE_SC)
                             sc_stage[sst + (uint32_t)(16 * r + it * (GPI / 8) * 4)] = (uint8_t)e;
