@@ -481,6 +481,48 @@ def _check_norm_rope(dev, q, k, wq, wk, f, got_q, got_k):
     assert_bits_equal(got_k, rk)
 
 
+# Every launch split of k_norm_rope: head dim 64 / 128 / 256, and head counts
+# that take two vectors per lane (D >= 128, H % (1024 / D) == 0), two or three
+# rows per lane with whole waves, or the masked kernel; with and without V and
+# a cached prefix (which needs V).
+@pytest.mark.parametrize("d,h,with_v,p", [(128, 24, False, 0), (128, 8, True, 4), (128, 12, False, 0),
+                                          (128, 20, True, 3), (128, 4, False, 0), (64, 16, False, 0),
+                                          (64, 24, True, 0), (64, 32, False, 0), (64, 10, True, 2),
+                                          (256, 8, False, 0), (256, 4, True, 1), (256, 6, True, 0),
+                                          (256, 5, False, 0)])
+def test_norm_rope_pack_every_split(dev, d, h, with_v, p):
+    g = torch.Generator().manual_seed(97)
+    b, s = 2, 37
+    q = bf16_randn(g, (b, s, h, d))
+    k = bf16_randn(g, (b, s, h, d))
+    v = bf16_randn(g, (b, s, h, d)) if with_v else None
+    ck = bf16_randn(g, (b, p, h, d)) if p else None
+    cv = bf16_randn(g, (b, p, h, d)) if p else None
+    wq = (torch.rand(d, generator=g) * 0.4 + 0.8).to(torch.bfloat16)
+    wk = (torch.rand(d, generator=g) * 0.4 + 0.8).to(torch.bfloat16)
+    phase = torch.randn(s, d // 2, generator=g)
+    freqs = torch.view_as_real(torch.polar(torch.ones_like(phase), phase)).reshape(s, d).contiguous()
+    say("norm_rope split", d, h, with_v, p)
+    dq, dk, dw_q, dw_k, df = (t.to(dev) for t in (q, k, wq, wk, freqs))
+    dv = v.to(dev) if with_v else None
+    dck = ck.to(dev) if p else None
+    dcv = cv.to(dev) if p else None
+    oq = torch.empty_like(dq)
+    ok = torch.empty((b, p + s, h, d), dtype=torch.bfloat16, device=dev)
+    ov = torch.empty_like(ok) if with_v else None
+    _native.call("qim_qk_norm_rope_pack", _native.ptr(dq), _native.ptr(dk), _native.ptr(dv), _native.ptr(dck),
+                 _native.ptr(dcv), _native.ptr(dw_q), _native.ptr(dw_k), _native.ptr(df), _native.ptr(oq),
+                 _native.ptr(ok), _native.ptr(ov), b, s, p, h, d, h * d, 1e-6, 1e-6, _native.stream())
+    rq, rk, rv = O.norm_rope_pack(bits(q), bits(k), bits(v) if with_v else bits(q), bits(wq), bits(wk),
+                                  freqs.numpy(), bits(ck) if p else None, bits(cv) if p else None)
+    assert_bits_equal(bits(oq), rq)
+    if with_v:
+        assert_bits_equal(bits(ok), rk)
+        assert_bits_equal(bits(ov), rv)
+    else:
+        assert_bits_equal(bits(ok)[:, p:], rk[:, p:])
+
+
 def test_prepare_attention_inputs_fallbacks(dev):
     """None for unsupported inputs (check_attention_ops.py:37-41)."""
     g = torch.Generator().manual_seed(721)
