@@ -1,0 +1,141 @@
+"""Teacher-forced replay (benchmarks/teacher_forced.py) on the GPU: the
+stand-in pipeline -- four blocks 512 wide, 4 heads of 128, FFN 1024, 256
+tokens against a 37-token prefix, 8 flow-matching Euler steps -- traced with
+the baseline profile (eager torch) and replayed through the `fused` and
+`mxfp8` profiles, whose blocks run on this build's kernels, and through a
+control: eager with float64 norm statistics.  Measured velocity rel-RMSE
+(mean over 8 steps, two starting latents): control 1.36 / 1.32 %, fused
+1.27 / 1.34 %, mxfp8 8.29 / 8.29 %.  Along the path of an eager MXFP8
+emulation instead: mxfp8 4.52 / 4.52 %, the emulation's own control 3.29 /
+3.78 %.  Random weights, so the figures are this stand-in's, not the
+product's (the reference's on the real model: fused 0, mxfp8 mean 1.735 %,
+max 4.162 %)."""
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import oracle as O
+from qwen_image_accel import _native, pipeline, replay
+from tests import fake_qwen21 as fq
+
+pytestmark = pytest.mark.gpu
+
+_SHAPE = dict(steps=8, n_blocks=4, dim=512, heads=4, ffn=1024, tokens=256, prefix=37)
+
+
+def _float64_norms(transformer):
+    """A control: the eager blocks with their LayerNorm and Q/K RMSNorm
+    statistics taken in float64 instead of torch's fp32 reduction -- an equally
+    valid rounding of the same formulas, the kind of difference the kernels'
+    exact statistics make."""
+    def layer_norm(m):
+        return lambda x: F.layer_norm(x.double(), m.normalized_shape, eps=m.eps).to(x.dtype)
+
+    def rms_norm(m):
+        def f(x):
+            y = x.double() * torch.rsqrt(x.double().pow(2).mean(-1, keepdim=True) + m.eps)
+            return y.to(m.weight.dtype) * m.weight
+        return f
+
+    for b in transformer.transformer_blocks:
+        b.img_norm1.forward, b.img_norm2.forward = layer_norm(b.img_norm1), layer_norm(b.img_norm2)
+        b.attn.norm_q.forward, b.attn.norm_k.forward = rms_norm(b.attn.norm_q), rms_norm(b.attn.norm_k)
+
+
+def test_teacher_forced_profiles(dev, monkeypatch):
+    print("[case] teacher-forced replay: baseline -> control, fused, mxfp8", flush=True)
+    monkeypatch.setenv("QW21_MXFP8_SKIP_BLOCKS", "")
+
+    def make(profile):
+        pipe, _ = fq.make_pipeline(device=dev, **_SHAPE)
+        if profile == "control":
+            _float64_norms(pipe.transformer)
+            profile = "baseline"
+        pipeline.install_hot_path(pipe.transformer, profile, validate=False)
+        return pipe
+
+    _, x0 = fq.make_pipeline(device=dev, **_SHAPE)
+    cases = {"a": lambda p: p(x0.clone()), "b": lambda p: p(x0.flip(1).contiguous())}
+    before = dict(_native.calls)
+    with torch.no_grad():
+        rep = replay.teacher_forced(make, ["control", "fused", "mxfp8"], cases)
+    used = {k for k, v in _native.calls.items() if v > before.get(k, 0)}
+    for profile, by_case in rep.items():
+        for case, r in by_case.items():
+            print(profile, case, {k: round(v, 6) for k, v in r.items() if k != "per_step"}, r["per_step"],
+                  flush=True)
+    assert {"qim_adaln", "qim_qk_norm_rope_pack", "qim_swiglu", "qim_adaln_quantize",
+            "qim_mxfp8_gemm_ex"} <= used, used
+    for case in cases:
+        control, fused, mx = rep["control"][case], rep["fused"][case], rep["mxfp8"][case]
+        assert len(fused["per_step"]) == len(mx["per_step"]) == _SHAPE["steps"]
+        # the fused profile differs from eager by no more than eager differs
+        # from itself with float64 norm statistics (both ~1.3 % here: a 1-ulp
+        # flip of the bf16 stream is ~6 % of the velocity's RMS where it lands)
+        assert fused["relative_rmse_mean"] < 1.5 * control["relative_rmse_mean"], (control, fused)
+        assert fused["relative_rmse_max"] < 3e-2, fused
+        # MXFP8 adds the quantization of every GEMM operand (~8 % here)
+        assert mx["relative_rmse_mean"] > 3 * control["relative_rmse_mean"], (control, mx)
+        assert mx["relative_rmse_max"] < 0.15, mx
+
+
+def _mx_roundtrip(t):
+    """The oracle's MXFP8 quantize then dequantize of a bf16 (rows, K) tensor,
+    as fp32 on t's device."""
+    bits = t.detach().contiguous().view(torch.int16).cpu().numpy().view("uint16")
+    q, sc = O.mx_quantize(bits)
+    return torch.from_numpy(O.mx_dequantize(q, sc, rows=t.shape[0])).to(t.device)
+
+
+def _emulate_mxfp8(transformer, acc=torch.float32):
+    """Eager blocks whose seven linears multiply the MXFP8 round trips of their
+    input rows and weight rows, accumulating in `acc` (the oracle's quantizer):
+    what the mxfp8 profile computes, up to where it rounds."""
+    def linear(lin):
+        w = _mx_roundtrip(lin.weight).to(acc)
+
+        def f(x):
+            xq = _mx_roundtrip(x.reshape(-1, x.shape[-1])).to(acc)
+            return (xq @ w.t()).to(x.dtype).reshape(*x.shape[:-1], -1)
+        return f
+
+    for b in transformer.transformer_blocks:
+        for lin in (b.attn.to_q, b.attn.to_k, b.attn.to_v, b.attn.to_out[0], b.img_mlp.proj,
+                    b.img_mlp.gate_layer, b.img_mlp.out):
+            lin.forward = linear(lin)
+
+
+def test_teacher_forced_mxfp8_against_emulation(dev, monkeypatch):
+    """The mxfp8 profile replayed along the path of its own emulation (eager
+    blocks with MXFP8 round trips of every linear's operands), beside the
+    emulation with float64 norm statistics and float64 GEMM accumulation as
+    the control: a bf16-level
+    difference before a quantizer moves some E4M3 codes by a whole code step
+    (2^-4 to 2^-3 relative), so the floor between two valid roundings of the
+    MXFP8 block is several times the bf16 one.  The kernels must sit at that
+    floor: the ~8 % against bf16 eager is the quantization itself."""
+    print("[case] teacher-forced replay: emulated mxfp8 -> control, mxfp8", flush=True)
+    monkeypatch.setenv("QW21_MXFP8_SKIP_BLOCKS", "")
+
+    def make(profile):
+        pipe, _ = fq.make_pipeline(device=dev, **_SHAPE)
+        if profile in ("emulated", "control"):
+            _emulate_mxfp8(pipe.transformer, torch.float64 if profile == "control" else torch.float32)
+            if profile == "control":
+                _float64_norms(pipe.transformer)
+            profile = "baseline"
+        pipeline.install_hot_path(pipe.transformer, profile, validate=False)
+        return pipe
+
+    _, x0 = fq.make_pipeline(device=dev, **_SHAPE)
+    cases = {"a": lambda p: p(x0.clone()), "b": lambda p: p(x0.flip(1).contiguous())}
+    with torch.no_grad():
+        rep = replay.teacher_forced(make, ["control", "mxfp8"], cases, baseline="emulated")
+    for profile, by_case in rep.items():
+        for case, r in by_case.items():
+            print(profile, "vs emulated", case, {k: round(v, 6) for k, v in r.items() if k != "per_step"},
+                  r["per_step"], flush=True)
+    for case in cases:
+        control, mx = rep["control"][case], rep["mxfp8"][case]
+        assert mx["relative_rmse_mean"] < 1.5 * control["relative_rmse_mean"], (control, mx)
+        assert mx["relative_rmse_max"] < 0.06, mx

@@ -1,0 +1,86 @@
+"""Teacher-forced replay (benchmarks/teacher_forced.py) on the CPU with the
+stand-in pipeline: the error metric against closed forms, the forcing of the
+latents, and the restoring of the pipeline's methods."""
+import pytest
+import torch
+
+from qwen_image_accel import pipeline, replay
+from tests import fake_qwen21 as fq
+
+
+def _run(latents):
+    return lambda pipe: pipe(latents.clone())
+
+
+def test_relative_rmse_closed_form():
+    """c = r (1 + e_i) gives exactly |e_i| per step."""
+    g = torch.Generator().manual_seed(3)
+    ref = [torch.randn(4, 33, generator=g, dtype=torch.float64) for _ in range(4)]
+    eps = [0.0, 1e-3, -0.25, 0.5]
+    rep = replay.relative_rmse(ref, [r * (1 + e) for r, e in zip(ref, eps)])
+    assert rep["relative_rmse_first"] == 0.0
+    assert rep["relative_rmse_max"] == pytest.approx(0.5, rel=1e-12)
+    assert rep["relative_rmse_last"] == pytest.approx(0.5, rel=1e-12)
+    assert rep["relative_rmse_mean"] == pytest.approx(sum(abs(e) for e in eps) / 4, rel=1e-12)
+    assert rep["per_step"] == [0.0, 0.001, 0.25, 0.5]
+    # an orthogonal error of the same norm: sqrt(2) - 1 would be wrong, 1 is right
+    r = torch.tensor([[1.0, 0.0]])
+    assert replay.relative_rmse([r], [torch.tensor([[1.0, 1.0]])])["relative_rmse_max"] == 1.0
+    with pytest.raises(ValueError):
+        replay.relative_rmse(ref, ref[:2])
+
+
+def test_trace_records_every_step_and_restores():
+    pipe, x0 = fq.make_pipeline(steps=5)
+    with torch.no_grad():
+        vel, lat = replay.trace(pipe, _run(x0))
+    assert len(vel) == 5 and len(lat) == 5
+    assert "forward" not in vars(pipe.transformer) and "step" not in vars(pipe.scheduler)
+    # the recorded latents are the sampler's own: x_{i+1} = x_i + dt_i v_i
+    x = x0
+    for i in range(5):
+        dt = float(pipe.scheduler.sigmas[i + 1] - pipe.scheduler.sigmas[i])
+        x = (x.float() + dt * vel[i]).to(x0.dtype)
+        assert torch.equal(x, lat[i])
+
+
+def test_replay_forces_the_baseline_latents():
+    """A candidate whose own sampler drifts still sees the baseline's latents:
+    its velocities equal the baseline's bit for bit (error exactly 0)."""
+    base, x0 = fq.make_pipeline(steps=4)
+    cand, _ = fq.make_pipeline(steps=4)
+    step = cand.scheduler.step
+    cand.scheduler.step = lambda v, i, s: ((step(v, i, s)[0].float() * 1.5).to(s.dtype),)
+    with torch.no_grad():
+        vel, lat = replay.trace(base, _run(x0))
+        free, _ = replay.trace(cand, _run(x0))
+        forced, none = replay.trace(cand, _run(x0), replay=lat)
+    assert none == []
+    assert replay.relative_rmse(vel, free)["relative_rmse_max"] > 0.01
+    assert replay.relative_rmse(vel, forced)["relative_rmse_max"] == 0.0
+    assert "step" in vars(cand.scheduler)   # an instance attribute before tracing stays one
+
+
+def test_replay_too_short_raises_and_restores():
+    pipe, x0 = fq.make_pipeline(steps=3)
+    with torch.no_grad():
+        _, lat = replay.trace(pipe, _run(x0))
+        with pytest.raises(IndexError, match="replay holds 2"):
+            replay.trace(pipe, _run(x0), replay=lat[:2])
+    assert "forward" not in vars(pipe.transformer) and "step" not in vars(pipe.scheduler)
+
+
+def test_teacher_forced_fused_on_cpu_is_exact():
+    """On CPU tensors the fused profile's kernels take the eager fallbacks, so
+    its replay error is exactly 0 (the reference reports 0 for `fused`)."""
+    def make(profile):
+        pipe, _ = fq.make_pipeline(steps=3)
+        pipeline.install_hot_path(pipe.transformer, profile, validate=False)
+        return pipe
+
+    _, x0 = fq.make_pipeline(steps=3)
+    with torch.no_grad():
+        rep = replay.teacher_forced(make, ["fused"], {"a": _run(x0), "b": _run(-x0)})
+    assert set(rep) == {"fused"} and set(rep["fused"]) == {"a", "b"}
+    for case in rep["fused"].values():
+        assert case["relative_rmse_max"] == 0.0 and len(case["per_step"]) == 3
