@@ -289,9 +289,13 @@ __device__ __forceinline__ float rstd_of(float var, float eps) {
 // complex rotation of the pairs (x[2j], x[2j+1]), reference
 // kernels/bf16.py:52-55 and kernels/elementwise.py:53-56).
 //
-// The sum of squares is taken in float64: for bf16 inputs it is exact, so it
-// does not depend on how the lanes of a row are reduced; it is rounded once to
-// the fp32 mean.
+// The sum of squares is taken in float64.  The square of a bf16 value has at
+// most 16 significant bits, so the sum of a 128-value row is exact while its
+// nonzero squares lie within 2^30 of each other, and it then does not depend on
+// how the lanes of a row are reduced; it is rounded once to the fp32 mean.
+// With a wider spread the smallest squares are rounded at 2^-53 of the sum, and
+// another reduction order can change the fp32 mean only when the exact value
+// lies within that distance of an fp32 rounding boundary.
 // (The square of a bf16 value is exact in float64, so the fused multiply-add
 // rounds exactly as a multiply then an add would.)
 __device__ __forceinline__ double head_sumsq8(const float *x) {

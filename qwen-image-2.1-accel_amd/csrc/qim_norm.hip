@@ -464,8 +464,9 @@ __device__ __forceinline__ void norm_rope_chunks(const uint4 (&xv)[V], uint4 (&o
 #pragma unroll
     for (int v = 0; v < V; ++v) unpack8(xv[v], x[v]);
     if constexpr (NORM) {
-        // The float64 sum of the squares of bf16 values is exact, so adding
-        // the chunks' sums first leaves it unchanged.
+        // The float64 sum of the squares of bf16 values is exact (short of a
+        // 2^30 spread of the squares), so adding the chunks' sums first leaves
+        // it unchanged.
         double ss = head_sumsq8(x[0]);
 #pragma unroll
         for (int v = 1; v < V; ++v) ss += head_sumsq8(x[v]);

@@ -416,7 +416,8 @@ def test_rms_norm(dev, mag):
     w = (torch.rand(128, generator=g) * 0.4 + 0.8).to(torch.bfloat16)
     say("rms_norm", mag)
     out = bf16.rms_norm(x.to(dev), w.to(dev), 1e-6)
-    # The float64 sum of squares of bf16 values is exact: bit-exact vs the oracle.
+    # The float64 sums of squares agree with the oracle's to 2^-53 of the sum (exactly where a row's
+    # squares lie within 2^30), so the fp32 statistics match: bit-exact vs the oracle.
     assert_bits_equal(bits(out), O.rms_norm(bits(x), bits(w)))
 
 
@@ -469,7 +470,8 @@ def test_prepare_attention_inputs(dev, b, s, p, h, mag):
 def _check_norm_rope(dev, q, k, wq, wk, f, got_q, got_k):
     """Fused RMSNorm + RoPE == RoPE of the separate rms_norm kernel's output
     (the invariant fused == separate) and == the oracle's RMSNorm then RoPE,
-    bit for bit (the float64 sum of squares is exact, so the fused and the
+    bit for bit (the float64 sums of squares agree to 2^-53 of the sum --
+    exactly where a row's squares lie within 2^30 -- so the fused and the
     separate kernel and the oracle share the fp32 statistic)."""
     nq = bf16.rms_norm(q.to(dev), wq.to(dev), 1e-6)
     nk = bf16.rms_norm(k.to(dev), wk.to(dev), 1e-6)
