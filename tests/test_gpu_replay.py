@@ -139,3 +139,32 @@ def test_teacher_forced_mxfp8_against_emulation(dev, monkeypatch):
         control, mx = rep["control"][case], rep["mxfp8"][case]
         assert mx["relative_rmse_mean"] < 1.5 * control["relative_rmse_mean"], (control, mx)
         assert mx["relative_rmse_max"] < 0.06, mx
+
+
+def test_teacher_forced_with_qim_attention(dev, monkeypatch):
+    """QW21_ATTENTION_BACKEND=qim: the profiles' attention runs on this build's
+    flash-attention core (bf16, and for mxfp8 writing the out-projection's
+    MXFP8 input).  Replayed along eager bf16's path: fused 1.69 % (1.27 % with
+    the default fp32 attention: the core's bf16 P adds a little), mxfp8 8.29 %
+    (unchanged)."""
+    print("[case] teacher-forced replay: baseline -> fused, mxfp8 with qim attention", flush=True)
+    monkeypatch.setenv("QW21_MXFP8_SKIP_BLOCKS", "")
+    monkeypatch.setenv("QW21_ATTENTION_BACKEND", "qim")
+
+    def make(profile):
+        pipe, _ = fq.make_pipeline(device=dev, **_SHAPE)
+        pipeline.install_hot_path(pipe.transformer, profile, validate=False)
+        return pipe
+
+    _, x0 = fq.make_pipeline(device=dev, **_SHAPE)
+    before = dict(_native.calls)
+    with torch.no_grad():
+        rep = replay.teacher_forced(make, ["fused", "mxfp8"], {"a": lambda p: p(x0.clone())})
+    used = {k for k, v in _native.calls.items() if v > before.get(k, 0)}
+    for profile, by_case in rep.items():
+        r = by_case["a"]
+        print(profile, "qim attention", {k: round(v, 6) for k, v in r.items() if k != "per_step"}, r["per_step"],
+              flush=True)
+    assert {"qim_attention", "qim_attention_mxfp8"} <= used, used
+    assert rep["fused"]["a"]["relative_rmse_max"] < 3e-2, rep["fused"]["a"]
+    assert rep["mxfp8"]["a"]["relative_rmse_max"] < 0.15, rep["mxfp8"]["a"]
