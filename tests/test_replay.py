@@ -84,3 +84,48 @@ def test_teacher_forced_fused_on_cpu_is_exact():
     assert set(rep) == {"fused"} and set(rep["fused"]) == {"a", "b"}
     for case in rep["fused"].values():
         assert case["relative_rmse_max"] == 0.0 and len(case["per_step"]) == 3
+
+
+
+class _Out:
+    def __init__(self, sample):
+        self.prev_sample = sample
+
+
+class _ObjScheduler(fq.FlowEulerScheduler):
+    """Returns an object with `prev_sample`, as Diffusers' schedulers do unless
+    return_dict=False; `factor` makes a drifting sampler."""
+
+    def __init__(self, steps, factor=1.0):
+        super().__init__(steps)
+        self.factor = factor
+
+    def step(self, velocity, index, sample):
+        x = super().step(velocity, index, sample)[0]
+        return _Out((x.float() * self.factor).to(sample.dtype))
+
+
+class _ObjPipeline(fq.StandInPipeline):
+    def __call__(self, latents):
+        for i in range(self.steps):
+            v = self.transformer(latents, float(self.scheduler.sigmas[i]))[0]
+            latents = self.scheduler.step(v, i, latents).prev_sample
+        return latents
+
+
+def test_scheduler_output_objects_are_forced_too():
+    """Replay replaces `prev_sample` on a scheduler output object."""
+    pipes = []
+    for factor in (1.0, 0.5):
+        p, x0 = fq.make_pipeline(steps=3)
+        obj = _ObjPipeline(p.transformer, 3)
+        obj.scheduler = _ObjScheduler(3, factor)
+        pipes.append(obj)
+    base, cand = pipes
+    with torch.no_grad():
+        vel, lat = replay.trace(base, _run(x0))
+        free, _ = replay.trace(cand, _run(x0))
+        forced, _ = replay.trace(cand, _run(x0), replay=lat)
+    assert len(lat) == 3 and all(isinstance(t, torch.Tensor) for t in lat)
+    assert replay.relative_rmse(vel, free)["relative_rmse_max"] > 0.01
+    assert replay.relative_rmse(vel, forced)["relative_rmse_max"] == 0.0
