@@ -170,19 +170,23 @@ class StandInTransformer(nn.Module):
         super().__init__()
         self.transformer_blocks = t.transformer_blocks
         self.dtype = t.dtype
-        _, mod, self.freqs, self.cache = inputs
+        _, mod, freqs, cache = inputs
         d = mod.shape[-1] // 4
         mod = mod.float().clone()
         mod[:, d:2 * d] *= 10
         mod[:, 3 * d:] *= 10
-        self.mod = mod.to(t.dtype)
+        # buffers, so that .to(device) moves them with the blocks
+        self.register_buffer("mod", mod.to(t.dtype))
+        self.register_buffer("freqs", freqs)
+        self.register_buffer("cache_k", cache.k)
+        self.register_buffer("cache_v", cache.v)
 
     def forward(self, hidden_states, sigma):
         h = hidden_states
         mod = (self.mod.float() * (1.0 + sigma)).to(self.mod.dtype)
+        cache = LayerCache(self.cache_k, self.cache_v)
         for b in self.transformer_blocks:
-            h = b(hidden_states=h, modulation=mod, rotary_emb=self.freqs, layer_cache=self.cache,
-                  kv_cache_mode="cached")
+            h = b(hidden_states=h, modulation=mod, rotary_emb=self.freqs, layer_cache=cache, kv_cache_mode="cached")
         return (h - hidden_states,)
 
 

@@ -168,3 +168,28 @@ def test_teacher_forced_with_qim_attention(dev, monkeypatch):
     assert {"qim_attention", "qim_attention_mxfp8"} <= used, used
     assert rep["fused"]["a"]["relative_rmse_max"] < 3e-2, rep["fused"]["a"]
     assert rep["mxfp8"]["a"]["relative_rmse_max"] < 0.15, rep["mxfp8"]["a"]
+
+
+def test_configure_pipeline_end_to_end(dev, monkeypatch):
+    """The reference's entry point on a whole (stand-in) pipeline: built on the
+    host, configure_pipeline moves the transformer to the GPU and installs the
+    profile; configured once only; the baseline-vs-mxfp8 replay through the
+    configured pipelines matches the install_hot_path figure (~8.3 %)."""
+    print("[case] configure_pipeline: baseline, mxfp8 on host-built pipelines", flush=True)
+    monkeypatch.setenv("QW21_MXFP8_SKIP_BLOCKS", "")
+    pipes = {}
+    for profile in ("baseline", "mxfp8"):
+        pipe, x0 = fq.make_pipeline(**_SHAPE)
+        cfg = pipeline.configure_pipeline(pipe, profile)
+        assert pipe._qw_optimization is cfg and cfg["profile"] == profile
+        assert all(t.is_cuda for t in pipe.transformer.state_dict().values())
+        pipes[profile] = pipe
+    assert pipes["mxfp8"]._qw_optimization["mxfp8_linears"] == 4 * 7
+    with pytest.raises(RuntimeError, match="once"):
+        pipeline.configure_pipeline(pipes["mxfp8"], "fused")
+    x0 = x0.to(dev)
+    with torch.no_grad():
+        rep = replay.teacher_forced(lambda p: pipes[p], ["mxfp8"], {"a": lambda p: p(x0.clone())})
+    r = rep["mxfp8"]["a"]
+    print("configured mxfp8", {k: round(v, 6) for k, v in r.items() if k != "per_step"}, flush=True)
+    assert 0.02 < r["relative_rmse_mean"] < 0.15, r

@@ -129,3 +129,16 @@ def test_scheduler_output_objects_are_forced_too():
     assert len(lat) == 3 and all(isinstance(t, torch.Tensor) for t in lat)
     assert replay.relative_rmse(vel, free)["relative_rmse_max"] > 0.01
     assert replay.relative_rmse(vel, forced)["relative_rmse_max"] == 0.0
+
+
+def test_configure_pipeline_needs_a_gpu_for_kernel_profiles():
+    """configure_pipeline (pipeline.py:109-198) validates before it changes
+    anything: without a ROCm GPU the kernel profiles are refused and the
+    pipeline stays unconfigured."""
+    if torch.cuda.is_available():
+        pytest.skip("checks the CPU-only refusal")
+    pipe, _ = fq.make_pipeline(steps=2)
+    for profile in ("fused", "mxfp8"):
+        with pytest.raises(RuntimeError, match="ROCm GPU"):
+            pipeline.configure_pipeline(pipe, profile)
+    assert not hasattr(pipe, "_qw_optimization") and "_qw_hot_path" not in vars(pipe.transformer)
