@@ -106,6 +106,15 @@ def test_abi_version():
                              None), _native.QIM_ERR_ARG),
     ("qim_attention_mxfp8", (16, 3072, 16, 3072, 16, 3072, 8, 16, 1, 16, 1 << 40, 1, 256, 256, 24, 128, 0.1,
                              None), _native.QIM_ERR_LAYOUT),
+    # size limits: a GEMM output stride of 2^25 elements; N * K = 2^31 code bytes; a quantizer row of 2^23
+    # elements (65536 scale blocks of 128); 2^30 heads of norm + RoPE
+    ("qim_mxfp8_gemm", (16, 16, 16, 16, 4, 256, 128, 0, None, None, None, 0, 16, 1 << 25, None, None),
+     _native.QIM_ERR_LAYOUT),
+    ("qim_mxfp8_gemm", (16, 16, 16, 16, 4, 1 << 16, 1 << 15, 0, None, None, None, 0, 16, 1 << 16, None, None),
+     _native.QIM_ERR_SHAPE),
+    ("qim_mx_quantize", (16, 1 << 23, 1, 1 << 23, 16, 16, None), _native.QIM_ERR_SHAPE),
+    ("qim_qk_norm_rope_pack", (16, 16, None, None, None, 16, 16, 16, 16, 16, None, 1, 4, 0, 1 << 30, 128,
+                               1 << 37, 1e-6, 1e-6, None), _native.QIM_ERR_SHAPE),
     # attention without a workspace: v required; a problem above the scratch array (S = T = 16640, 24 heads)
     ("qim_attention_noalloc", (16, 3072, 16, 3072, None, 3072, 16, 3072, 1, 256, 256, 24, 128, 0.1, None),
      _native.QIM_ERR_ARG),
