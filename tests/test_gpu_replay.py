@@ -193,3 +193,29 @@ def test_configure_pipeline_end_to_end(dev, monkeypatch):
     r = rep["mxfp8"]["a"]
     print("configured mxfp8", {k: round(v, 6) for k, v in r.items() if k != "per_step"}, flush=True)
     assert 0.02 < r["relative_rmse_mean"] < 0.15, r
+
+
+def test_teacher_forced_model_dims(dev, monkeypatch):
+    """The replay at the model's own widths: two stand-in blocks 3072 wide, 24
+    heads of 128, FFN 12288, one 1024^2 image's 4352 tokens against a 256-token
+    prefix, 3 steps (random weights, so again the stand-in's figures).
+    Measured: fused 0.56 %, mxfp8 8.64 % (mean over the steps)."""
+    print("[case] teacher-forced replay at D 3072 / 24 heads / 4352 tokens", flush=True)
+    monkeypatch.setenv("QW21_MXFP8_SKIP_BLOCKS", "")
+    shape = dict(steps=3, n_blocks=2, dim=3072, heads=24, ffn=12288, tokens=4352, prefix=256)
+
+    def make(profile):
+        pipe, _ = fq.make_pipeline(device=dev, **shape)
+        pipeline.install_hot_path(pipe.transformer, profile, validate=False)
+        return pipe
+
+    _, x0 = fq.make_pipeline(device=dev, **shape)
+    with torch.no_grad():
+        rep = replay.teacher_forced(make, ["fused", "mxfp8"], {"a": lambda p: p(x0.clone())})
+    for profile, by_case in rep.items():
+        r = by_case["a"]
+        print(profile, "model dims", {k: round(v, 6) for k, v in r.items() if k != "per_step"}, flush=True)
+    fused, mx = rep["fused"]["a"], rep["mxfp8"]["a"]
+    assert fused["relative_rmse_max"] < 3e-2, fused
+    assert mx["relative_rmse_max"] < 0.15, mx
+    assert mx["relative_rmse_mean"] > 3 * fused["relative_rmse_mean"], (fused, mx)
