@@ -260,6 +260,101 @@ def bench_quantize(steps, warmup):
                 frac=nbytes / us / 1e3 / HBM_PEAK_GBS, shape="[4352,3072]")
 
 
+def bench_adaln_quantize(steps, warmup, M=4352, D=3072, separate=False, block_form=False):
+    """a6, layer_norm_scale_quantize(x, scale, norm) (kernels/epilogue.py:
+    76-92): MXFP8(bf16(LN(x) * scale)) of x [M, D] ~N(0,1) (every 512th
+    column x25, as the reference's check), scale [1, D] ~N(0,1), row-major
+    codes.  ``separate``: the two launches the fusion replaces (qim_adaln,
+    then qim_mx_quantize of its bf16 output; tests/gpu/check_mx_epilogue.py:
+    48-61 times the same pair).  ``block_form``: the config-5 block's call
+    (precomputed 1 + s, + shift, tiled codes)."""
+    from qwen_image_accel import _native
+    g = torch.Generator(device="cuda").manual_seed(505)   # device-side draws: large inputs, timing only
+    nbytes = 2 * M * D + M * D + M * D // 32 + 2 * D * (2 if block_form else 1)
+    n = copies_for(2 * M * D)
+    xs = []
+    for _ in range(n):
+        x = torch.randn(M, D, generator=g, device="cuda")
+        x[:, ::512] *= 25
+        xs.append(x.to(torch.bfloat16))
+    scale = torch.randn(1, D, generator=g, device="cuda").to(torch.bfloat16)
+    shift = (0.1 * torch.randn(1, D, generator=g, device="cuda")).to(torch.bfloat16) if block_form else None
+    qs = [torch.empty(M, D, dtype=torch.uint8, device="cuda") for _ in range(n)]
+    ss = [torch.empty(M * D // 32, dtype=torch.uint8, device="cuda") for _ in range(n)]
+    mid = torch.empty(M, D, dtype=torch.bfloat16, device="cuda") if separate else None
+    L = _native.lib()
+    flags = _native.ADALN_TILED if block_form else 0
+
+    def step(i):
+        j = i % n
+        st = torch.cuda.current_stream().cuda_stream
+        if separate:
+            rc = L.qim_adaln(xs[j].data_ptr(), scale.data_ptr(), None, None, None, mid.data_ptr(), M, D, M, 1e-6, 0,
+                             st)
+            rc = rc or L.qim_mx_quantize(mid.data_ptr(), D, M, D, qs[j].data_ptr(), ss[j].data_ptr(), st)
+        else:
+            rc = L.qim_adaln_quantize(xs[j].data_ptr(), scale.data_ptr(), shift.data_ptr() if block_form else None,
+                                      None, None, qs[j].data_ptr(), ss[j].data_ptr(), M, D, M, 1e-6, flags, st)
+        assert rc == 0
+    us = Timed(step, steps, warmup).run() * 1e3
+    return dict(kernel="qim_adaln + qim_mx_quantize" if separate else "qim_adaln_quantize", us=us, bytes=nbytes,
+                gbs=nbytes / us / 1e3, frac=nbytes / us / 1e3 / HBM_PEAK_GBS,
+                shape=f"[{M},{D}]" + (" +shift, tiled (the block's call)" if block_form else ""))
+
+
+def bench_swiglu_quantize(steps, warmup, M=4352, F=12288, separate=False, strided=True):
+    """a12, swiglu_quantize(g, v) (kernels/epilogue.py:123-136):
+    MXFP8(bf16(bf16(silu g) * v)), row-major codes.  ``strided``: g and v
+    are the two halves of config 3's [M, 2F] projection (as the block's
+    unfused form); else two contiguous [M, F] tensors (the reference's check,
+    tests/gpu/check_mx_epilogue.py:56-61).  ``separate``: qim_swiglu, then
+    qim_mx_quantize of its bf16 output."""
+    from qwen_image_accel import _native
+    g = torch.Generator(device="cuda").manual_seed(91)    # device-side draws: large inputs, timing only
+    nbytes = 4 * M * F + M * F + M * F // 32
+    n = copies_for(4 * M * F)
+    xs = [torch.randn(M, 2 * F, generator=g, device="cuda").to(torch.bfloat16) for _ in range(n)]
+    qs = [torch.empty(M, F, dtype=torch.uint8, device="cuda") for _ in range(n)]
+    ss = [torch.empty(M * F // 32, dtype=torch.uint8, device="cuda") for _ in range(n)]
+    mid = torch.empty(M, F, dtype=torch.bfloat16, device="cuda") if separate else None
+    L = _native.lib()
+    if strided:
+        ops = [(x.data_ptr(), x.data_ptr() + 2 * F, 2 * F) for x in xs]
+    else:   # contiguous g and v: the first M*F and the next M*F elements of each buffer
+        ops = [(x.data_ptr(), x.data_ptr() + 2 * M * F, F) for x in xs]
+
+    def step(i):
+        j = i % n
+        st = torch.cuda.current_stream().cuda_stream
+        gp, vp, ld = ops[j]
+        if separate:
+            rc = L.qim_swiglu(gp, ld, vp, ld, mid.data_ptr(), F, M, F, st)
+            rc = rc or L.qim_mx_quantize(mid.data_ptr(), F, M, F, qs[j].data_ptr(), ss[j].data_ptr(), st)
+        else:
+            rc = L.qim_swiglu_quantize(gp, ld, vp, ld, qs[j].data_ptr(), ss[j].data_ptr(), M, F, st)
+        assert rc == 0
+    us = Timed(step, steps, warmup).run() * 1e3
+    return dict(kernel="qim_swiglu + qim_mx_quantize" if separate else "qim_swiglu_quantize", us=us, bytes=nbytes,
+                gbs=nbytes / us / 1e3, frac=nbytes / us / 1e3 / HBM_PEAK_GBS,
+                shape=f"[{M},{F}] x2 " + ("(halves of [M, 2F])" if strided else "(contiguous)") + " -> MXFP8")
+
+
+def bench_mx_epilogue_check(steps, warmup):
+    """The reference's fused-against-separate timing of its MXFP8 epilogues
+    (tests/gpu/check_mx_epilogue.py:48-61): LN x scale -> MXFP8 at D = 4096
+    and SwiGLU -> MXFP8 at F = 12288 (contiguous g, v), M = 1024, 4096,
+    16384, each fused and as the two launches it replaces; µs per call."""
+    out = {}
+    for m in (1024, 4096, 16384):
+        for kind, fn in (("layernorm", bench_adaln_quantize), ("swiglu", bench_swiglu_quantize)):
+            kw = dict(M=m, D=4096) if kind == "layernorm" else dict(M=m, F=12288, strided=False)
+            fused = fn(steps, warmup, **kw)["us"]
+            sep = fn(steps, warmup, separate=True, **kw)["us"]
+            out[f"{kind}_M{m}"] = {"fused_us": round(fused, 2), "separate_us": round(sep, 2),
+                                   "saved_us": round(sep - fused, 2)}
+    return out
+
+
 def bench_gemm(steps, warmup, tiled=True, rotate=True):
     """Config 4b: MXFP8 GEMM [4352 x 3072] x [3072 x 12288] + bias.  ``tiled``:
     both operands in the tiled code layout MXFP8Linear uses (weight quantized
@@ -606,6 +701,12 @@ def main():
                      ("swiglu_1024", lambda: bench_swiglu(steps, warm)),
                      ("gated_residual_1024", lambda: bench_residual(steps, warm)),
                      ("quantize_1024", lambda: bench_quantize(steps, warm)),
+                     ("adaln_quantize_1024", lambda: bench_adaln_quantize(steps, warm)),
+                     ("adaln_quantize_1024_block_form", lambda: bench_adaln_quantize(steps, warm, block_form=True)),
+                     ("adaln_quantize_1024_separate", lambda: bench_adaln_quantize(steps, warm, separate=True)),
+                     ("swiglu_quantize_1024", lambda: bench_swiglu_quantize(steps, warm)),
+                     ("swiglu_quantize_1024_separate", lambda: bench_swiglu_quantize(steps, warm, separate=True)),
+                     ("mx_epilogue_check", lambda: bench_mx_epilogue_check(max(20, steps // 4), warm)),
                      ("mxfp8_gemm_bias_1024", lambda: bench_gemm(steps, warm)),
                      ("mxfp8_gemm_bias_1024_warm", lambda: bench_gemm(steps, warm, rotate=False)),
                      ("mxfp8_gemm_bias_1024_rowmajor", lambda: bench_gemm(steps, warm, tiled=False)),
@@ -622,16 +723,18 @@ def main():
                      ("copy_40.5MB", lambda: bench_copy_ceiling(steps, warm, 40525824, "40.5 MB moved")),
                      ("copy_80.2MB", lambda: bench_copy_ceiling(steps, warm, 80222208, "80.2 MB moved")),
                      ("copy_109MB", lambda: bench_copy_ceiling(steps, warm, 109183488, "109.2 MB moved")),
+                     ("copy_269MB", lambda: bench_copy_ceiling(steps, warm, 269058048, "269.1 MB moved")),
                      ("copy_320.9MB", lambda: bench_copy_ceiling(steps, warm, 320864256, "320.9 MB moved"))]:
         if not want(name):
             continue
         log(f"[bench] {name} ...")
         try:
             comp[name] = fn()
-        except Exception as exc:  # the vendor reference may be missing on some stacks; ours never is
+        except Exception as exc:  # the vendor reference may fail on some stacks; ours never may
             if not name.endswith("reference_scaled_mm"):
                 raise
-            log(f"[bench] {name} unavailable: {exc!r}")
+            log(f"[bench] {name} failed: {exc!r}")
+            comp[name] = {"error": f"{type(exc).__name__}: {str(exc).strip().splitlines()[0][:300]}"}
             continue
         log(f"[bench] {name}: {json.dumps(comp[name])}")
         torch.cuda.empty_cache()
@@ -664,10 +767,16 @@ def main():
                                              "dispatch, each scaled by its reading for a 256 MiB copy"}
     # Each bandwidth-bound op against the fastest copy moving the same bytes in one launch.
     same_size_copy = {"adaln_512": "copy_23.6MB", "quantize_1024": "copy_40.5MB",
+                      "adaln_quantize_1024": "copy_40.5MB", "adaln_quantize_1024_block_form": "copy_40.5MB",
+                      "adaln_quantize_1024_separate": "copy_40.5MB",
+                      "swiglu_quantize_1024": "copy_269MB", "swiglu_quantize_1024_separate": "copy_269MB",
                       "gated_residual_1024": "copy_80.2MB", "qk_norm_rope_1024": "copy_109MB",
                       "swiglu_1024": "copy_320.9MB"}
     summary = {}
     for k, v in comp.items():
+        if "us" not in v:          # a failed reference call, or a table of timings
+            summary[k] = v
+            continue
         e = {"us": round(v["us"], 2)}
         if "gbs" in v:
             e.update(GBs=round(v["gbs"], 1), hbm_frac=round(v["frac"], 4))

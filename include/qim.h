@@ -257,7 +257,11 @@ int qim_attention_mxfp8(const void *q, int64_t ldq, const void *k, int64_t ldk, 
  * qim_attention_workspace_bytes exceeds the maximum is rejected with
  * QIM_ERR_SHAPE before anything is launched (S = T = 4352 with 24 heads fits
  * for one batch).  Every call on a device shares its array: calls that
- * overlap on one device race. */
+ * overlap on one device race.  The first call on each device resolves the
+ * array's device address (hipGetSymbolAddress, which may make the runtime
+ * load the library's code object and place the array on that device): make
+ * that first call before any graph capture begins, so that a captured call
+ * only launches kernels. */
 #define QIM_ATTENTION_NOALLOC_MAX_BYTES (64ll << 20)
 int qim_attention_noalloc(const void *q, int64_t ldq, const void *k, int64_t ldk, const void *v, int64_t ldv,
                           void *o, int64_t ldo, int64_t B, int64_t S, int64_t T, int64_t H, int64_t D,

@@ -346,14 +346,14 @@ __device__ __forceinline__ void tile_of(const GemmArgs &p, int &tm, int &tn) {
 // The SwiGLU epilogues look bf16(silu(g)) up instead of computing it (the
 // estimate, its band test and the rounding cost ~14 vector instructions per
 // output, on one wave per SIMD with nothing to hide them).  The table holds
-// every bf16 g with biased exponent 101..132 (2^-26 <= |g| < 128): entry i of
+// every bf16 g with biased exponent 101..132 (2^-26 <= |g| < 64): entry i of
 // a sign is g = bits 0x3280 + i, positive at byte 2i, negative at 8192 + 2i,
 // so for the packed bf16 pair G the two byte addresses come from
 // P = G - 0x3280 (per half) as (P << 1) for bits 0..12 and (P >> 2) for the
 // sign at bit 13; a value is in the table when bits 12..14 of P are clear.
 // Entries are computed with silu_bf16 (bit-identical to the reference's
 // rounding) by each workgroup while its first stages' loads are in flight;
-// the rest (|g| < 2^-26, |g| >= 128, NaN) takes silu_bf16 itself.
+// the rest (|g| < 2^-26, |g| >= 64, NaN) takes silu_bf16 itself.
 constexpr int SILU_TAB_BYTES = 16384;
 constexpr uint16_t SILU_TAB_BASE = 0x3280;
 typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));

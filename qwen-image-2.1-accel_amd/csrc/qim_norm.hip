@@ -43,22 +43,30 @@ constexpr int ADALN_FULL_WAVES = 4;    // full-coverage kernels: 256 threads, no
 constexpr uint32_t BF16X2_NEG_ZERO = 0x80008000u, BF16X2_ONE = 0x3f803f80u;
 
 // The biased variance of a row, rounded to fp32, from one pass: S2 = sum(x^2)
-// and mean_d = fl(S1 / D).  The reference value is fl32(fl(V / D)), V the
-// float64 two-pass sum of (x - mean_d)^2 in any order.  Both that value and
-// v1 = S2 / D - mean_d^2 (evaluated below) lie within
-//   E = (2D + 32) 2^-53 (|v1| + mean_d^2) (1 + 2^-20)
-// of sum((x - mean_d)^2) / D: the two-pass sum of D positive terms, each
-// rounded three times, is within (D + 3) 2^-53 of it relatively; S2 (D - 1
-// additions of exact squares), the product by fl(1/D), mean_d^2 and the
-// subtraction give (D + 2) 2^-53 of the variance plus (D + 4) 2^-53 of
-// mean^2.  When v1 - E and v1 + E round to the same fp32 value, so does the
-// reference value (rounding is monotonic), and it is returned; otherwise
-// (false) the caller runs the second pass.  NaN or infinite sums give a NaN
-// interval end, which compares unequal.
+// and mean_d = fl(S1 / D), S1 the float64 sum of the row in any order.  The
+// reference value is fl32(fl(V / D)), V the float64 two-pass sum of
+// (x - mean_d)^2 in any order.  Both that value and v1 = S2 / D - mean_d^2
+// (evaluated below) lie within
+//   E = (4D + 32) 2^-53 (|v1| + mean_d^2) (1 + 2^-20)
+// of sum((x - mean_d)^2) / D = S2/D - mean_d^2 + 2 mean_d (mean_d - sum(x)/D):
+//  - the two-pass sum of D positive terms, each rounded three times, is within
+//    (D + 3) 2^-53 of it relatively;
+//  - S2 (D - 1 additions of exact squares), the product by fl(1/D), mean_d^2
+//    and the subtraction give (D + 2) 2^-53 of the variance plus (D + 4) 2^-53
+//    of mean^2;
+//  - the last term: mean_d is within 2^-53 |mean_d| of S1 / D, and S1 within
+//    (D - 1) 2^-53 sum|x| <= (D - 1) 2^-53 sqrt(D S2) of the exact sum (S1 is
+//    exact only while the row's values lie within about 2^(45 - log2 D) of
+//    each other), so the term is at most 2^-52 mean_d^2 +
+//    (D - 1) 2^-52 |mean_d| sqrt(S2 / D) <= (2D - 1) 2^-53 (mean_d^2 + |v|).
+// When v1 - E and v1 + E round to the same fp32 value, so does the reference
+// value (rounding is monotonic), and it is returned; otherwise (false) the
+// caller runs the second pass.  NaN or infinite sums give a NaN interval end,
+// which compares unequal.
 __device__ __forceinline__ bool ln_variance(double s2, double mean_d, int D, double inv_d, float &var) {
     const double sq = mean_d * mean_d;
     const double v1 = s2 * inv_d - sq;
-    const double e = (2.0 * D + 32.0) * 0x1p-53 * (__builtin_fabs(v1) + sq) * (1.0 + 0x1p-20);
+    const double e = (4.0 * D + 32.0) * 0x1p-53 * (__builtin_fabs(v1) + sq) * (1.0 + 0x1p-20);
     const float lo = (float)(v1 - e), hi = (float)(v1 + e);
     var = lo;
     return lo == hi;

@@ -143,6 +143,17 @@ def test_modulation_values_exhaustive(dev):
         nan_w = (w & 0x7f80 == 0x7f80) & (w & 0x7f != 0)
         assert np.array_equal(nan_g, nan_w), k
         assert np.array_equal(g[~nan_g], w[~nan_w]), (k, int((g[~nan_g] != w[~nan_w]).sum()))
+    # The cached-decode path (optimizations/decode.py) keeps torch's bf16
+    # tanh, as the reference's precompute does (optimizations/fusion.py:48-53).
+    # Count where torch's on-device tanh differs from the kernel's (printed
+    # for the record; the CPU tanh equals the kernel's definition on every
+    # input, tests/test_parity_bar.py).  At most a few last-bit differences.
+    dev_tanh = bits(allb.to(dev).tanh().cpu().reshape(64, 1024)).astype(np.int64)
+    live = ~((got["tanh"] & 0x7f80 == 0x7f80) & (got["tanh"] & 0x7f != 0))
+    diff = got["tanh"][live] != dev_tanh[live]
+    print(f"tanh: kernel vs torch on-device bf16 tanh differ on {int(diff.sum())} of {int(live.sum())} inputs, "
+          f"max {int(np.abs(got['tanh'][live] - dev_tanh[live]).max())} ulp")
+    assert np.abs(got["tanh"][live] - dev_tanh[live]).max() <= 1
 
 
 def test_silu_exhaustive(dev):
@@ -346,6 +357,31 @@ def test_adaln_second_pass_rows(dev, d):
     shift, scale, gate = (bf16_randn(g, (1, 1, d), 0.1) for _ in range(3))
     res = bf16_randn(g, (1, 300, d))
     say("adaln second pass", d)
+    out = layernorm.layer_norm_scale(x.to(dev), scale.to(dev), _LN(d), shift=shift.to(dev),
+                                     gate=gate.to(dev), residual=res.to(dev), add_one=True)
+    assert_bits_equal(bits(out), O.adaln(bits(x), bits(scale), bits(shift), bits(gate), bits(res), add_one=True))
+    fused = epilogue.layer_norm_scale_quantize(x.to(dev), scale.to(dev), _LN(d))
+    q, sc = O.adaln_quantize(bits(x), bits(scale))
+    assert np.array_equal(u8(fused.values), q)
+    assert np.array_equal(u8(fused.scales), sc)
+
+
+def test_adaln_wide_rows(dev):
+    """Rows whose values span 2^-60 .. 2^60, so the float64 row sum S1 is no
+    longer exact (the one-pass variance bound then includes S1's rounding),
+    beside rows with a few 2^60 outliers among N(0, 1) values and rows of
+    2^50 offsets over 2^-60 noise: bit-exact against the oracle (whose mean
+    agrees with the kernel's after the fp32 rounding of the statistics)."""
+    g = torch.Generator().manual_seed(60)
+    d = 3072
+    x = torch.randn(1, 96, d, generator=g)
+    x[0, 0::3] *= torch.exp2(torch.randint(-60, 61, (32, d), generator=g).float())
+    x[0, 1::3, ::700] = torch.randn(32, 5, generator=g) * 2.0 ** 60
+    x[0, 2::3] = x[0, 2::3] * 2.0 ** -60 + 2.0 ** 50
+    x = x.to(torch.bfloat16)
+    scale, shift, gate = (bf16_randn(g, (1, 1, d), 0.1) for _ in range(3))
+    res = bf16_randn(g, (1, 96, d))
+    say("adaln wide rows")
     out = layernorm.layer_norm_scale(x.to(dev), scale.to(dev), _LN(d), shift=shift.to(dev),
                                      gate=gate.to(dev), residual=res.to(dev), add_one=True)
     assert_bits_equal(bits(out), O.adaln(bits(x), bits(scale), bits(shift), bits(gate), bits(res), add_one=True))
@@ -672,6 +708,17 @@ def test_mxfp8_gemm_bias_config4(dev):
     ref = O.mx_gemm(u8(aq.values), u8(aq.scales), u8(wq.values), u8(wq.scales), rows=rows)
     ref = ref + bf16_values(bits(bias))[None, :]
     assert rel_fro(y.float().cpu().numpy()[rows], ref) < 1e-2
+    # The path bench.py times: both operands quantized straight into the tiled
+    # layout, the same bias epilogue.  Codes and scales equal the row-major
+    # quantization's, and the product equals the row-major one bit for bit
+    # (same MFMAs in the same order), so it is the oracle's within the bar.
+    say("gemm bias config4 tiled")
+    at = mxfp8.quantize(a.to(dev), tiled=True)
+    wt = mxfp8.quantize(w.to(dev), tiled=True)
+    assert torch.equal(mxfp8.as_row_major(at).values, aq.values) and torch.equal(at.scales, aq.scales)
+    yt = gemm.mx_matmul(at, wt.values, wt.scales, epilogue="bias", bias=bias.to(dev), weight_tiled=True)
+    assert_bits_equal(bits(yt), bits(y))
+    assert rel_fro(yt.float().cpu().numpy()[rows], ref) < 1e-2
 
 
 def test_mxfp8_gemm_gated_residual(dev):

@@ -72,3 +72,39 @@ def test_no_alloc_attention_rejects_problems_above_its_scratch(dev):
                                               0.1, None)
     assert rc == _native.QIM_ERR_SHAPE
     assert b"scratch" in _native.lib().qim_last_error()
+
+
+def test_no_alloc_attention_under_graph_capture(dev):
+    """The use it is for: a call captured in a HIP graph.  The first call on
+    the device (made before the capture) resolves the scratch array; the
+    captured call then allocates nothing, and every replay, with the
+    program's own eager work between replays, equals qim_attention bit for
+    bit."""
+    g = torch.Generator().manual_seed(77)
+    b, s, t, h = 1, 1100, 1300, 6
+    say("attention noalloc graph", b, s, t, h)
+    q, kv = _inputs(g, b, s, t, h, dev)
+    ref = _with_workspace(q, kv, b, s, t, h)
+    o = torch.empty(b, s, h, 128, dtype=torch.bfloat16, device=dev)
+    row = 2 * h * 128
+
+    def call():
+        _native.call("qim_attention_noalloc", _native.ptr(q), h * 128, _native.ptr(kv), row,
+                     ctypes_offset(kv, h * 128), row, _native.ptr(o), h * 128, b, s, t, h, 128, 128 ** -0.5,
+                     _native.stream(q.device))
+
+    call()                                   # first call on the device: before any capture
+    torch.cuda.synchronize()
+    assert torch.equal(o.view(torch.int16), ref.view(torch.int16))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call()
+    for r in range(3):
+        o.fill_(float("nan"))                # eager work between replays
+        other = _with_workspace(q, kv, b, s, t, h)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(o.view(torch.int16), ref.view(torch.int16)), f"replay {r}"
+        assert torch.equal(other.view(torch.int16), ref.view(torch.int16))
+    del graph
