@@ -425,10 +425,13 @@ def test_swiglu_strided_halves_config3(dev):
     assert_bits_equal(bits(out), O.swiglu(bits(X[:, :12288]), bits(X[:, 12288:])))
 
 
-@pytest.mark.parametrize("rows,width", [(1024, 12288), (2400, 12288), (16384, 12288), (128, 12288), (77, 256)])
+@pytest.mark.parametrize("rows,width", [(1024, 12288), (2400, 12288), (16384, 12288), (128, 12288), (77, 256),
+                                        (130, 384)])
 def test_swiglu_quantize(dev, rows, width):
     """Fused == quantize(swiglu) byte for byte (check_mx_epilogue.py:40-46,
-    the same shapes), and codes and scales bit-exact against the oracle."""
+    the same shapes), and codes and scales bit-exact against the oracle.
+    (130, 384): three 128-column chunks, so a workgroup's four waves span
+    two row groups, and padding rows 130..255."""
     g = torch.Generator().manual_seed(0)
     a = bf16_randn(g, (rows, width))
     v = bf16_randn(g, (rows, width))
@@ -441,6 +444,22 @@ def test_swiglu_quantize(dev, rows, width):
     q, s = O.swiglu_quantize(bits(a), bits(v))
     assert np.array_equal(u8(fused.values), q)
     assert np.array_equal(u8(fused.scales), s)
+
+
+def test_swiglu_quantize_over_grid_y_limit(dev):
+    """262,344 rows: 65,600 row groups of four rows, above the 65,535 of one
+    launch's grid y, so the launcher splits the rows over two launches; fused
+    == quantize(swiglu) byte for byte, row-major and tiled."""
+    g = torch.Generator(device=dev).manual_seed(3)
+    rows = 262144 + 200
+    a = torch.randn(rows, 128, generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn(rows, 128, generator=g, device=dev).to(torch.bfloat16)
+    say("swiglu_quantize grid fold", rows, 128)
+    for tiled in (False, True):
+        fused = epilogue.swiglu_quantize(a, v, tiled=tiled)
+        sep = mxfp8.quantize(bf16.swiglu(a, v), tiled=tiled)
+        assert torch.equal(fused.values.view(torch.uint8), sep.values.view(torch.uint8))
+        assert torch.equal(fused.scales.view(torch.uint8), sep.scales.view(torch.uint8))
 
 
 # ------------------------------------------------------ RMSNorm, RoPE --
