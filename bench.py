@@ -412,14 +412,27 @@ def bench_scaled_mm(steps, warmup):
     sa = torch.full((M, K // 32), 127, dtype=torch.uint8, device="cuda").view(torch.float8_e8m0fnu)
     sb = torch.full((N, K // 32), 127, dtype=torch.uint8, device="cuda").view(torch.float8_e8m0fnu)
 
+    # The reference's call has a bf16 output.  hipBLASLt's heuristic can pick
+    # a backend that refuses that output's scale type (one driver box:
+    # "rocRoller only supports F32 as scale type not Half",
+    # HIPBLAS_STATUS_INVALID_VALUE); the call is then timed with an fp32
+    # output, the same products, and the bf16 error is recorded beside it.
+    out_dtype, notes = torch.bfloat16, {}
+    try:
+        torch._scaled_mm(sets[0][0], sets[0][1].t(), scale_a=sa, scale_b=sb, out_dtype=out_dtype)
+        torch.cuda.synchronize()
+    except RuntimeError as e:
+        notes = {"bf16_output_error": str(e).splitlines()[0][:300]}
+        out_dtype = torch.float32
+
     def step(i):
         a, b = sets[i % n]
-        torch._scaled_mm(a, b.t(), scale_a=sa, scale_b=sb, out_dtype=torch.bfloat16)
+        torch._scaled_mm(a, b.t(), scale_a=sa, scale_b=sb, out_dtype=out_dtype)
     us = Timed(step, n * max(1, -(-10 // n)), warmup).run() * 1e3
     flops = 2 * M * N * K
     tf = flops / us / 1e6
     return dict(kernel="torch._scaled_mm (hipBLASLt)", us=us, flops=flops, tflops=tf, frac=tf / MXFP8_PEAK_TFLOPS,
-                shape="4352x3072x12288", operand_sets=n)
+                shape="4352x3072x12288", operand_sets=n, out_dtype=str(out_dtype).replace("torch.", ""), **notes)
 
 
 def bench_attention(tokens, steps, warmup):
@@ -787,8 +800,23 @@ def main():
                 e["variant"] = v["variant"]
         if "tflops" in v:
             e.update(TFLOPs=round(v["tflops"], 1), mfma_frac=round(v.get("frac", v.get("gemm_frac")), 4))
+        for key in ("out_dtype", "bf16_output_error"):
+            if key in v:
+                e[key] = v[key]
         summary[k] = e
     out["components"] = summary
+    # The metric names three parts; `value` is the first.  All three side by side:
+    parts = {}
+    if "qk_norm_rope_1024" in summary:
+        parts.update(fused_op_GBs=summary["qk_norm_rope_1024"]["GBs"],
+                     fused_op_hbm_frac=summary["qk_norm_rope_1024"]["hbm_frac"])
+    if "mxfp8_gemm_bias_1024" in summary:
+        parts.update(mxfp8_gemm_TFLOPs=summary["mxfp8_gemm_bias_1024"]["TFLOPs"],
+                     mxfp8_gemm_mfma_frac=summary["mxfp8_gemm_bias_1024"]["mfma_frac"])
+    if "block_1024" in summary:
+        parts.update(us_per_block_1024=summary["block_1024"]["us"])
+    if parts:
+        out["metric_parts"] = parts
     if want("cpu"):
         log("[bench] cpu baseline ...")
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds,

@@ -165,77 +165,96 @@ __global__ __launch_bounds__(64 * W) void k_quant_tile(Source src, uint8_t *__re
         *reinterpret_cast<uint4 *>(chunk0 + lane * 16) = reinterpret_cast<const uint4 *>(sb)[lane];
 }
 
-// The SwiGLU quantizer's kernel: one 16-byte vector of g and of v per lane
-// and no loop.  A wave owns rows r, r + 32, r + 64, r + 96 of a 128-row tile
-// (r < 32) over one 128-column chunk, lanes 16j .. 16j + 15 holding row
-// r + 32j, 8 columns each; its 16 exponents (4 rows x 4 blocks of 32) are
-// then the 16 contiguous bytes r * 16 .. r * 16 + 15 of the tile's 512-byte
-// scale chunk: lane 16j gathers row j's four by DPP row shifts, and the four
-// dword stores of one instruction cover the 16 bytes.  The four waves of a
-// workgroup take four consecutive column chunks of the same rows, and
+// The SwiGLU quantizer's kernel: U 16-byte vectors of g and of v per lane
+// (U = 2, or 1 for an odd chunk count), all loads issued first.  A wave owns
+// rows r, r + 32, r + 64, r + 96 of a 128-row tile (r < 32) over U adjacent
+// 128-column chunks, lanes 16j .. 16j + 15 holding row r + 32j, 8 columns of
+// each chunk.  Per chunk its 16 exponents (4 rows x 4 blocks of 32) are the
+// 16 contiguous bytes r * 16 .. r * 16 + 15 of that tile's 512-byte scale
+// chunk: lane 16j gathers row j's four by DPP row shifts, and the four dword
+// stores of one instruction cover the 16 bytes.  The four waves of a
+// workgroup take four adjacent U-chunk groups of the same rows, and
 // consecutive workgroups the next four.  Rows in [M, Mp) read as zeros
-// (codes 0, the exponent of 0), as in k_quant_tile.  The SiLU makes this
+// (codes 0, the exponent of 0), as in k_quant_tile.  The 32 groups of a
+// scale chunk come from 32 workgroups, and the scale bytes reach HBM about
+// twice (3 % of the launch's writes).  The SiLU makes this
 // source arithmetic-heavy (~24 vector instructions per element), and many
 // short waves overlap it with the loads better than k_quant_tile's eight rows
-// per lane: [4352, 12288] 54.7 -> 47.5 us, [16640, 12288] 212 -> 175 us (same
-// box; addresses, tile and row in scalar registers, no division).  The plain
-// quantizer stays on k_quant_tile (8.55 against 9.4 us in this form).
-template <class Source>
+// per lane: [4352, 12288] 54.7 -> 46.1 us, [16640, 12288] 212 -> 162 us (same
+// box; addresses, tile and row in scalar registers, no division, U = 2; one
+// chunk per lane measured 47.5 / 175 us, four 47.5 / 172 us).  The plain
+// quantizer stays on k_quant_tile (8.53 against 9.0-10.0 us in this form).
+template <class Source, int U>
 __global__ __launch_bounds__(256) void k_quant_rows(Source src, uint8_t *__restrict__ q,
                                                     uint8_t *__restrict__ scales, int64_t M, int64_t K,
                                                     int64_t Mp, uint32_t nk, int tiled, int64_t g0) {
     const int lane = threadIdx.x & 63, j = lane >> 4, c16 = lane & 15;
     // Wave-uniform position (scalar registers): the four waves of a workgroup
-    // take column chunks tc = 4 blockIdx.x .. + 3 of the same rows, and
-    // consecutive workgroups the next chunks (walking along the rows, as a
-    // copy would); row r32 of each quarter of tile tr from g0 + blockIdx.y.
-    const uint32_t tc = blockIdx.x * 4 + (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    if (tc >= nk) return;  // the last workgroup of a row when nk % 4 != 0 (wave-uniform, no barrier)
+    // take column-chunk groups tcu = 4 blockIdx.x .. + 3 (chunks U tcu ..
+    // U tcu + U - 1) of the same rows, and consecutive workgroups the next
+    // groups (walking along the rows, as a copy would); row r32 of each
+    // quarter of tile tr from g0 + blockIdx.y.
+    const uint32_t tcu = blockIdx.x * 4 + (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if ((tcu + 1) * U > nk) return;  // past the last group of a row (wave-uniform, no barrier)
     const int64_t grp = g0 + blockIdx.y;
     const int64_t tr = grp >> 5;
     const int r32 = (int)(grp & 31);
     const int64_t row0 = tr * 128 + r32;           // the wave's first row; lane rows row0 + 32 j
     const int64_t row = row0 + j * 32;
-    uint4 a, b;
-    src.load_at(row0, j, (int64_t)tc * 128 + c16 * 8, row < M, a, b);
-    int e;
-    const uint2 c = src.quantize(a, b, e);
-    // Code offset: row-major row * K + col, or mxt_offset(row, col, Mp, K),
-    // whose 256-row super-block (r0, n rows) and chunk swizzle (bits 1-3 of
-    // the row: those of r32) are the wave's.
-    int64_t off;
-    if (tiled) {
-        const int64_t r0 = (tr * 128) & ~int64_t(255);
-        const int64_t n = Mp - r0 < 256 ? Mp - r0 : 256;
-        const int sw = mx_chunk_swizzle(row0);
-        off = r0 * K + ((int64_t)tc * 2 + (c16 >> 3)) * n * 64 + (row - r0) * 64 +
-              ((((c16 >> 1) & 3) ^ sw) << 4) + (c16 & 1) * 8;
-    } else {
-        off = row * K + (int64_t)tc * 128 + c16 * 8;
+    uint4 a[U], b[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) src.load_at(row0, j, (int64_t)(tcu * U + u) * 128 + c16 * 8, row < M, a[u], b[u]);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const uint32_t tc = tcu * U + u;
+        int e;
+        const uint2 c = src.quantize(a[u], b[u], e);
+        // Code offset: row-major row * K + col, or mxt_offset(row, col, Mp,
+        // K), whose 256-row super-block (r0, n rows) and chunk swizzle (bits
+        // 1-3 of the row: those of r32) are the wave's.
+        int64_t off;
+        if (tiled) {
+            const int64_t r0 = (tr * 128) & ~int64_t(255);
+            const int64_t n = Mp - r0 < 256 ? Mp - r0 : 256;
+            const int sw = mx_chunk_swizzle(row0);
+            off = r0 * K + ((int64_t)tc * 2 + (c16 >> 3)) * n * 64 + (row - r0) * 64 +
+                  ((((c16 >> 1) & 3) ^ sw) << 4) + (c16 & 1) * 8;
+        } else {
+            off = row * K + (int64_t)tc * 128 + c16 * 8;
+        }
+        st_nt(q + off, c);
+        const uint32_t e1 = dpp_mov<DPP_ROW_SHL4>((uint32_t)e);
+        const uint32_t e2 = dpp_mov<DPP_ROW_SHL8>((uint32_t)e);
+        const uint32_t e3 = dpp_mov<DPP_ROW_SHL12>((uint32_t)e);
+        if (c16 == 0)
+            *reinterpret_cast<uint32_t *>(scales + (tr * nk + tc) * 512 + r32 * 16 + j * 4) =
+                (uint32_t)e | (e1 << 8) | (e2 << 16) | (e3 << 24);
     }
-    st_nt(q + off, c);
-    const uint32_t e1 = dpp_mov<DPP_ROW_SHL4>((uint32_t)e);
-    const uint32_t e2 = dpp_mov<DPP_ROW_SHL8>((uint32_t)e);
-    const uint32_t e3 = dpp_mov<DPP_ROW_SHL12>((uint32_t)e);
-    if (c16 == 0)
-        *reinterpret_cast<uint32_t *>(scales + (tr * nk + tc) * 512 + r32 * 16 + j * 4) =
-            (uint32_t)e | (e1 << 8) | (e2 << 16) | (e3 << 24);
 }
 
-// Grid of k_quant_rows: ceil(K / 512) groups of four column chunks x
+// Grid of k_quant_rows: ceil(K / (512 U)) groups of four U-chunk groups x
 // (Mp / 128) * 32 row groups, workgroups of four waves; grid y is at most
-// 65535, so larger row counts take several launches.
-template <class Source>
-static void launch_quant_rows(const Source &src, uint8_t *q, uint8_t *scales, int64_t M, int64_t K, int tiled,
-                              hipStream_t st) {
+// 65535, so larger row counts take several launches.  U = 2 (two chunks per
+// lane, both loads issued first) when the chunk count is even, else 1.
+template <class Source, int U>
+static void launch_quant_rows_u(const Source &src, uint8_t *q, uint8_t *scales, int64_t M, int64_t K, int tiled,
+                                hipStream_t st) {
     const int64_t Mp = (M + 127) / 128 * 128;
     const uint32_t nk = (uint32_t)(K / 128);
     const int64_t groups = Mp / 128 * 32;
     for (int64_t g0 = 0; g0 < groups; g0 += 65535) {
         const int64_t n = groups - g0 < 65535 ? groups - g0 : 65535;
-        launch(k_quant_rows<Source>, dim3((nk + 3) / 4, (unsigned)n), dim3(256), 0, st, src, q, scales, M, K, Mp, nk,
-               tiled, g0);
+        launch(k_quant_rows<Source, U>, dim3((nk / U + 3) / 4, (unsigned)n), dim3(256), 0, st, src, q, scales, M, K,
+               Mp, nk, tiled, g0);
     }
+}
+template <class Source>
+static void launch_quant_rows(const Source &src, uint8_t *q, uint8_t *scales, int64_t M, int64_t K, int tiled,
+                              hipStream_t st) {
+    if ((K / 128) % 2 == 0)
+        launch_quant_rows_u<Source, 2>(src, q, scales, M, K, tiled, st);
+    else
+        launch_quant_rows_u<Source, 1>(src, q, scales, M, K, tiled, st);
 }
 
 // Workgroups of one wave (W = 1) or four (W = 4): the launch shape of the
