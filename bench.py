@@ -463,17 +463,19 @@ def bench_attention(tokens, steps, warmup):
                 shape=f"S=T={tokens}, 24x128")
 
 
-def bench_block(tokens, steps, warmup, with_attention=False, rotate=True):
+def bench_block(tokens, steps, warmup, with_attention=False, rotate=True, dim=3072, heads=24):
     """Config 5 / µs-per-block: one MMDiT block minus the attention core
     (with_attention: the whole block, the attention core included).
     ``rotate``: consecutive steps run different blocks -- enough of them that
     their MXFP8 weights (151 MB each) exceed twice the Infinity Cache, as the
     32 blocks of a model follow each other -- else one block, whose weights
-    then stay cache-resident across steps (a warm-cache best case)."""
+    then stay cache-resident across steps (a warm-cache best case).
+    ``dim``, ``heads``: 3072 / 24 is config 5; 4096 / 32 is the reference
+    model's own width (FFN 12288 in both)."""
     from qwen_image_accel import rope
     from qwen_image_accel.block import MMDiTBlock
     g = gen(42)
-    first = MMDiTBlock.random(g, device="cuda")
+    first = MMDiTBlock.random(g, dim=dim, heads=heads, device="cuda")
     wbytes = sum(q.values.numel() + q.scales.numel() for q in (first.w_qkv, first.w_out, first.w_gate_up,
                                                                 first.w_down))
     n = copies_for(wbytes) if rotate else 1
@@ -484,8 +486,8 @@ def bench_block(tokens, steps, warmup, with_attention=False, rotate=True):
         blocks.append(MMDiTBlock.from_weights(roll(w0["qkv"]), roll(w0["out"]), roll(w0["gate"]), roll(w0["up"]),
                                               roll(w0["down"]), w0["norm_q"], w0["norm_k"], first.heads))
     side = int(round(((tokens - 256)) ** 0.5))
-    h = randn(g, (1, tokens, 3072))
-    mod = randn(g, (1, 6, 3072), 0.1)
+    h = randn(g, (1, tokens, dim))
+    mod = randn(g, (1, 6, dim), 0.1)
     freqs = rope.image_table(256, side, side, "cuda")
 
     def step(i):
@@ -495,7 +497,7 @@ def bench_block(tokens, steps, warmup, with_attention=False, rotate=True):
     k_steps = n * max(1, -(-max(3, steps // 20) // n))
     us = Timed(step, k_steps, warmup).run() * 1e3
     flops = first.flops(tokens)
-    return dict(us=us, flops=flops, tflops=flops / us / 1e6, tokens=tokens,
+    return dict(us=us, flops=flops, tflops=flops / us / 1e6, tokens=tokens, dim=dim, heads=heads,
                 gemm_frac=flops / us / 1e6 / MXFP8_PEAK_TFLOPS, blocks=n,
                 cache="weights rotated past 2x the Infinity Cache" if rotate else "warm (one block)")
 
@@ -727,6 +729,7 @@ def main():
                      ("block_1024", lambda: bench_block(4352, steps, warm)),
                      ("block_1024_warm", lambda: bench_block(4352, steps, warm, rotate=False)),
                      ("block_2048", lambda: bench_block(16640, steps, warm)),
+                     ("block_1024_d4096", lambda: bench_block(4352, steps, warm, dim=4096, heads=32)),
                      ("attention_1024", lambda: bench_attention(4352, steps, warm)),
                      ("attention_2048", lambda: bench_attention(16640, steps, warm)),
                      ("block_1024_with_attention", lambda: bench_block(4352, steps, warm, with_attention=True)),

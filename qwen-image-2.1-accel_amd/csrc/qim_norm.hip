@@ -399,14 +399,27 @@ static int launch_adaln_rg(const AdaLNArgs &a, hipStream_t st) {
             launch((k_adaln<QUANT, 2, true, RG>), grid, dim3(64 * (k / 2)), 0, st, a);
             return QIM_OK;
         }
+        // The block's quantizing AdaLN (no residual or gate, the scale used as
+        // given) takes the PLAIN form at D = 3072 (NV 3) and D = 4096 (NV 4).
+        constexpr bool PLAIN_OK = QUANT && !RG;
+        const bool plain = PLAIN_OK && !(a.flags & QIM_ADALN_ADD_ONE);
         if (k % 3 == 0 && k / 3 <= ADALN_FULL_WAVES) {
-            if (QUANT && !RG && !(a.flags & QIM_ADALN_ADD_ONE))  // the block's quantizing AdaLN
-                launch((k_adaln<QUANT, 3, true, RG, false, true>), grid, dim3(64 * (k / 3)), 0, st, a);
-            else
-                launch((k_adaln<QUANT, 3, true, RG>), grid, dim3(64 * (k / 3)), 0, st, a);
+            if constexpr (PLAIN_OK) {
+                if (plain) {
+                    launch((k_adaln<QUANT, 3, true, RG, false, true>), grid, dim3(64 * (k / 3)), 0, st, a);
+                    return QIM_OK;
+                }
+            }
+            launch((k_adaln<QUANT, 3, true, RG>), grid, dim3(64 * (k / 3)), 0, st, a);
             return QIM_OK;
         }
         if (k % 4 == 0 && k / 4 <= ADALN_FULL_WAVES) {
+            if constexpr (PLAIN_OK) {
+                if (plain) {
+                    launch((k_adaln<QUANT, 4, true, RG, false, true>), grid, dim3(64 * (k / 4)), 0, st, a);
+                    return QIM_OK;
+                }
+            }
             launch((k_adaln<QUANT, 4, true, RG>), grid, dim3(64 * (k / 4)), 0, st, a);
             return QIM_OK;
         }

@@ -76,9 +76,12 @@ def assert_weight_equal(hip, ref, what):
     assert np.array_equal(rm.scales.view(torch.uint8).cpu().numpy(), ref[1]), what
 
 
-@pytest.mark.parametrize("b,s", [(1, 4352), (1, 16640)])
-def test_block_config5_against_oracle(dev, b, s):
-    dim, heads, ffn = 3072, 24, 12288
+@pytest.mark.parametrize("b,s,dim,heads", [(1, 4352, 3072, 24), (1, 16640, 3072, 24), (1, 4352, 4096, 32)])
+def test_block_config5_against_oracle(dev, b, s, dim, heads):
+    """Config 5's block (D 3072, 24 heads) at 1024^2 and 2048^2, and the
+    reference model's own width (D 4096 = 32 heads x 128, FFN 12288) at
+    1024^2."""
+    ffn = 12288
     side = int(round((s - 256) ** 0.5))
     say("block vs oracle", b, s, dim, heads, ffn)
     g = torch.Generator().manual_seed(42)
