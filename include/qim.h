@@ -193,6 +193,29 @@ int qim_mxfp8_gemm_ex(const void *aq, const void *as, const void *bq, const void
                       const void *bias, const void *gate, const void *res, int64_t seq,
                       void *out, int64_t ldo, void *out_scales, void *stream);
 
+/* qim_mxfp8_gemm_ex with a caller-provided workspace (no reference
+ * counterpart; the same call as optimizations/mxfp8.py:32-36).  When the
+ * tile grid's last partial round is a few quarter tiles (at most CUs / 2 of
+ * them; e.g. 272 tiles of 256 x 256 on 256 CUs) and the epilogue is
+ * QIM_EPI_NONE, QIM_EPI_BIAS or QIM_EPI_GATED_RESIDUAL, each of those quarter
+ * tiles is split over K between several workgroups that write fp32 partial
+ * sums to ws; a second launch on the same stream adds them in a fixed order
+ * and runs the epilogue.  The result is the same function of the inputs
+ * within the accumulation order (the partial sums of the tail are added in a
+ * different order than one workgroup's MFMA chain).  ws: 16-byte aligned, at
+ * least qim_mxfp8_gemm_ws_bytes(M, N, K, epilogue) bytes, not shared by calls
+ * that may overlap; with ws = NULL or a smaller ws_bytes the call is
+ * qim_mxfp8_gemm_ex. */
+int qim_mxfp8_gemm_ws(const void *aq, const void *as, const void *bq, const void *bs,
+                      int64_t M, int64_t N, int64_t K, int epilogue, int layouts,
+                      const void *bias, const void *gate, const void *res, int64_t seq,
+                      void *out, int64_t ldo, void *out_scales, void *ws, int64_t ws_bytes,
+                      void *stream);
+
+/* Workspace bytes qim_mxfp8_gemm_ws uses for this problem on the current
+ * device; 0 when it splits nothing. */
+int64_t qim_mxfp8_gemm_ws_bytes(int64_t M, int64_t N, int64_t K, int epilogue);
+
 /* The fused QKV projection of the MMDiT block: qim_mxfp8_gemm_ex with
  * N = 3 * H * 128 whose output columns [0, H*128) (Q) and [H*128, 2*H*128) (K)
  * leave the GEMM as rope(RMSNorm(bf16(acc))) per 128-wide head, exactly what

@@ -71,6 +71,12 @@ struct GemmArgs {
     // seq / 64 (seq % 64 == 0).
     uint16_t *vt;
     int64_t vt_nkb;
+    // Split-K tail (qim_mxfp8_gemm_ws): with ksplit > 1 each quarter tile of
+    // the last partial round is computed by ksplit workgroups over disjoint
+    // ranges of K, which write their fp32 accumulators to ws; k_mx_gemm_tail
+    // then sums them in a fixed order and runs the epilogue.
+    float *ws;
+    int ksplit;
 };
 
 // qim_mxfp8_gemm_qk_norm_rope_vt: the QK-norm + RoPE epilogue whose V columns
@@ -915,9 +921,18 @@ __device__ __forceinline__ void qstep(const GemmArgs &p, const QPlan &Q, uint8_t
 #undef QIM_QMF
 }
 
-template <int EPI>
-__device__ __forceinline__ void quarter_tile(const GemmArgs &p, uint8_t *lds, uint8_t *tab, int q) {
-    int64_t m0, n0;
+// fp32 words of one split-K partial: a quarter tile's 4 waves x 2 x 2 MFMA
+// tiles x 16 accumulators x 64 lanes, in register order (each store and load
+// instruction covers 256 contiguous bytes).
+constexpr int QPART_WORDS = 4 * 2 * 2 * 16 * 64;
+
+__device__ __forceinline__ float *qpart(const GemmArgs &p, int unit, int wave, int i, int j, int r, int lane) {
+    return p.ws + (int64_t)unit * QPART_WORDS + (((wave * 2 + i) * 2 + j) * 16 + r) * 64 + lane;
+}
+
+// Corner of quarter tile q (of the last whole tiles, or a 128-row piece of a
+// last 128-column block).
+__device__ __forceinline__ void quarter_origin(const GemmArgs &p, int q, int64_t &m0, int64_t &n0) {
     if (q < p.quarters) {  // a quarter of one of the last whole tiles
         const int tile = p.main_tiles + q / 4, quarter = q & 3;
         int tm, tn;
@@ -928,31 +943,53 @@ __device__ __forceinline__ void quarter_tile(const GemmArgs &p, uint8_t *lds, ui
         m0 = (int64_t)(q - p.quarters) * 128;
         n0 = (int64_t)p.tiles_n * BN;
     }
+}
+
+// Quarter-tile unit u: quarter tile u % quarters over K-stage pairs
+// [kp * P / ksplit, (kp + 1) * P / ksplit), kp = u / quarters, P = K / 128 (the
+// whole of K when ksplit == 1).  Stages keep their ring slot (s & 3) and
+// their parity (even stages carry the 128-K scale group).
+template <int EPI>
+__device__ __forceinline__ void quarter_tile(const GemmArgs &p, uint8_t *lds, uint8_t *tab, int u) {
+    const int split = p.ksplit > 1 ? p.ksplit : 1;
+    const int q = split > 1 ? u % p.quarters : u, kp = split > 1 ? u / p.quarters : 0;
+    int64_t m0, n0;
+    quarter_origin(p, q, m0, n0);
     if (m0 >= p.Mp) return;  // padding rows only (whole workgroup)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1, lr = lane & 31, kh = lane >> 5;
-    const int S = (int)(p.K / BK);
+    const int P = (int)(p.K / (2 * BK));
+    const int sb = 2 * (kp * P / split), se = 2 * ((kp + 1) * P / split);
     f32x16_t acc[2][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = f32x16_t{};
     const QPlan Q = make_qplan(p, m0, n0);
-    issue_qstage<true>(p, Q, lds, 0);
-    issue_qstage<false>(p, Q, lds + STAGE_BYTES, 1 < S ? 1 : S - 1);
-    issue_qstage<true>(p, Q, lds + 2 * STAGE_BYTES, 2 < S ? 2 : S - 1);
-    issue_qstage<false>(p, Q, lds + 3 * STAGE_BYTES, 3 < S ? 3 : S - 1);
+    issue_qstage<true>(p, Q, lds + (sb & 3) * STAGE_BYTES, sb);
+    issue_qstage<false>(p, Q, lds + ((sb + 1) & 3) * STAGE_BYTES, sb + 1);
+    issue_qstage<true>(p, Q, lds + ((sb + 2) & 3) * STAGE_BYTES, sb + 2 < se ? sb + 2 : se - 1);
+    issue_qstage<false>(p, Q, lds + ((sb + 3) & 3) * STAGE_BYTES, sb + 3 < se ? sb + 3 : se - 1);
     if constexpr (ring_offset<EPI>() > 0) fill_silu_table(tab);
-    wait_vmcnt<QLOADS_ODD + QLOADS_EVEN + QLOADS_ODD>();  // stage 0 landed
+    wait_vmcnt<QLOADS_ODD + QLOADS_EVEN + QLOADS_ODD>();  // stage sb landed
     block_barrier();
     QFrags fa, fb;
-    read_qfrags(lds, wm, wn, lr, kh, fa, true);
-    for (int s = 0; s < S; s += 2) {
-        qstep<0>(p, Q, lds, s, S, acc, fa, fb, wm, wn, lr, kh);
-        qstep<1>(p, Q, lds, s + 1, S, acc, fb, fa, wm, wn, lr, kh);
+    read_qfrags(lds + (sb & 3) * STAGE_BYTES, wm, wn, lr, kh, fa, true);
+    for (int s = sb; s < se; s += 2) {
+        qstep<0>(p, Q, lds, s, se, acc, fa, fb, wm, wn, lr, kh);
+        qstep<1>(p, Q, lds, s + 1, se, acc, fb, fa, wm, wn, lr, kh);
     }
     wait_vmcnt<0>();
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (split > 1) {  // a partial sum: to the workspace, the epilogue runs in k_mx_gemm_tail
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) *qpart(p, u, wave, i, j, r, lane) = acc[i][j][r];
+        return;
+    }
     block_barrier();
     epilogue<EPI, 2, 2>(p, acc, lds, tab, m0 + wm * 64, n0 + wn * 64, lane, wave);
 }
@@ -1004,11 +1041,54 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     epilogue<EPI, 4, 4>(p, acc, lds, tab, m0 + wm * 128, n0 + wn * 128, lane, wave);
 }
 
+// The split-K tail's second launch: one workgroup per quarter tile sums its
+// ksplit partials in order kp = 0, 1, ... (the register layout the quarter
+// tile's waves wrote) and runs the quarter tile's epilogue on them.  (One
+// one-wave workgroup per 64 x 64 block instead, four times as many, took
+// 48.5 us against 7.8 us at 64 quarter tiles x 4 splits.)
+constexpr int TAIL_LDS_BYTES = 4 * 16 * (64 * 8 + 8 * 16);  // epilogue<EPI, 2, 2>'s staging (TJ = 2, bf16 rows)
+
+template <int EPI>
+__global__ __launch_bounds__(256) void k_mx_gemm_tail(GemmArgs p) {
+    static_assert(ring_offset<EPI>() == 0, "the split tail runs the plain, bias and gated-residual epilogues");
+    __shared__ __attribute__((aligned(16))) uint8_t lds[TAIL_LDS_BYTES];
+    const int q = (int)blockIdx.x;
+    int64_t m0, n0;
+    quarter_origin(p, q, m0, n0);
+    if (m0 >= p.Mp) return;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    f32x16_t acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = *qpart(p, q, wave, i, j, r, lane);
+    for (int kp = 1; kp < p.ksplit; ++kp) {
+        const int u = kp * p.quarters + q;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] += *qpart(p, u, wave, i, j, r, lane);
+    }
+    epilogue<EPI, 2, 2>(p, acc, lds, nullptr, m0 + wm * 64, n0 + wn * 64, lane, wave);
+}
+
+// CUs the work split plans for: the current device's, or MI355X's 256 when no
+// device answers (sizes queried without a GPU).
+static int64_t plan_cus() {
+    const int c = device_cus();
+    return c > 0 ? c : 256;
+}
+
 // Whole tiles to launch: all of them, or all but the last r when the last
 // round of the CUs would hold r <= CUs / 2 tiles (those become 4r quarters).
 static int64_t main_tile_count(int64_t tiles) {
-    const int64_t cus = device_cus();
-    if (cus <= 0 || tiles <= cus) return tiles;
+    const int64_t cus = plan_cus();
+    if (tiles <= cus) return tiles;
     const int64_t r = tiles % cus;
     return (r > 0 && 2 * r <= cus) ? tiles - r : tiles;
 }
@@ -1021,9 +1101,29 @@ static int launch_gemm(const GemmArgs &a, hipStream_t st) {
                                    "qim_mxfp8_gemm"))
         return rc;
     const int64_t half_column = a.tiles_n * BN < a.N ? (a.Mp + 127) / 128 : 0;
-    const int64_t grid = a.main_tiles + a.quarters + half_column;
+    const int64_t split = a.ksplit > 1 ? a.ksplit : 1;
+    const int64_t grid = a.main_tiles + a.quarters * split + half_column;
     launch(k_mx_gemm<EPI>, dim3((unsigned)grid), dim3(256), lds_bytes, st, a);
+    if constexpr (ring_offset<EPI>() == 0 && EPI != QIM_EPI_QK_NORM_ROPE && EPI != EPI_QKV_VT) {
+        if (split > 1) launch(k_mx_gemm_tail<EPI>, dim3((unsigned)a.quarters), dim3(256), 0, st, a);
+    }
     return QIM_OK;
+}
+
+// K-splits of the tail's quarter tiles: as many as fill the CUs' one round
+// (quarters * ksplit <= CUs), at most one stage pair each and at most 8; 1
+// (no split) when the quarters alone hold more than half the CUs, when a last
+// 128-column block is there, or for an epilogue other than the plain, bias
+// and gated-residual ones.
+static int tail_ksplit(int64_t quarters, bool half_column, int epilogue, int64_t K) {
+    const int64_t cus = plan_cus();
+    if (quarters <= 0 || half_column) return 1;
+    if (epilogue != QIM_EPI_NONE && epilogue != QIM_EPI_BIAS && epilogue != QIM_EPI_GATED_RESIDUAL) return 1;
+    int64_t k = cus / quarters;
+    const int64_t pairs = K / (2 * BK);
+    if (k > pairs) k = pairs;
+    if (k > 8) k = 8;
+    return k >= 2 ? (int)k : 1;
 }
 
 }  // namespace qim
@@ -1038,9 +1138,18 @@ struct QKNormRope {
     void *vt;  // V^T tiles instead of the V columns of out, or null
 };
 
+// Quarter tiles and K-splits of the tail for a problem shape (tail_ksplit).
+static void tail_plan(int64_t M, int64_t N, int64_t K, int epilogue, int64_t &quarters, int &ksplit) {
+    const int64_t Mp = (M + 127) / 128 * 128, tiles_m = (Mp + BM - 1) / BM, tiles_n = N / BN;
+    const int64_t tiles = tiles_m * tiles_n;
+    quarters = 4 * (tiles - main_tile_count(tiles));
+    ksplit = tail_ksplit(quarters, tiles_n * BN < N, epilogue, K);
+}
+
 static int gemm_run(const void *aq, const void *as, const void *bq, const void *bs, int64_t M, int64_t N, int64_t K,
                     int epilogue, int layouts, const void *bias, const void *gate, const void *res, int64_t seq,
-                    void *out, int64_t ldo, void *out_scales, const QKNormRope *qk, void *stream) {
+                    void *out, int64_t ldo, void *out_scales, const QKNormRope *qk, void *stream,
+                    void *ws = nullptr, int64_t ws_bytes = 0) {
     QIM_REQUIRE(aq && as && bq && bs && out, QIM_ERR_ARG, "qim_mxfp8_gemm: null pointer");
     constexpr int KNOWN = QIM_GEMM_A_TILED | QIM_GEMM_B_TILED | QIM_GEMM_OUT_TILED | QIM_GEMM_OUT_F32 | QIM_GEMM_OUT_F16;
     QIM_REQUIRE((layouts & ~KNOWN) == 0, QIM_ERR_ARG, "qim_mxfp8_gemm: unknown layout flags 0x%x", layouts);
@@ -1087,6 +1196,16 @@ static int gemm_run(const void *aq, const void *as, const void *bq, const void *
     const int64_t tiles = tiles_m * tiles_n;
     a.main_tiles = (int)main_tile_count(tiles);
     a.quarters = (int)(4 * (tiles - a.main_tiles));
+    if (ws && !qk) {
+        int64_t quarters;
+        int ksplit;
+        tail_plan(M, N, K, epilogue, quarters, ksplit);
+        QIM_REQUIRE(aligned16(ws), QIM_ERR_LAYOUT, "qim_mxfp8_gemm_ws: ws must be 16-byte aligned");
+        if (ksplit > 1 && ws_bytes >= quarters * ksplit * (int64_t)QPART_WORDS * 4) {
+            a.ws = static_cast<float *>(ws);
+            a.ksplit = ksplit;
+        }
+    }
     int rc;
     switch (epilogue) {
         case QIM_EPI_NONE:
@@ -1143,6 +1262,22 @@ extern "C" int qim_mxfp8_gemm_ex(const void *aq, const void *as, const void *bq,
                                  void *stream) {
     return gemm_run(aq, as, bq, bs, M, N, K, epilogue, layouts, bias, gate, res, seq, out, ldo, out_scales, nullptr,
                     stream);
+}
+
+extern "C" int64_t qim_mxfp8_gemm_ws_bytes(int64_t M, int64_t N, int64_t K, int epilogue) {
+    if (M <= 0 || N <= 0 || K <= 0 || K % 128 || N % 128) return 0;
+    int64_t quarters;
+    int ksplit;
+    tail_plan(M, N, K, epilogue, quarters, ksplit);
+    return ksplit > 1 ? quarters * ksplit * (int64_t)QPART_WORDS * 4 : 0;
+}
+
+extern "C" int qim_mxfp8_gemm_ws(const void *aq, const void *as, const void *bq, const void *bs, int64_t M,
+                                 int64_t N, int64_t K, int epilogue, int layouts, const void *bias, const void *gate,
+                                 const void *res, int64_t seq, void *out, int64_t ldo, void *out_scales, void *ws,
+                                 int64_t ws_bytes, void *stream) {
+    return gemm_run(aq, as, bq, bs, M, N, K, epilogue, layouts, bias, gate, res, seq, out, ldo, out_scales, nullptr,
+                    stream, ws, ws_bytes);
 }
 
 static int qk_norm_rope_run(const char *who, const void *aq, const void *as, const void *bq, const void *bs, int64_t M,

@@ -60,6 +60,8 @@ SIGNATURES = {
     "qim_qk_norm_rope_pack": (_C, [_P] * 11 + [_I] * 6 + [_F, _F, _P]),
     "qim_mxfp8_gemm": (_C, [_P, _P, _P, _P, _I, _I, _I, _C, _P, _P, _P, _I, _P, _I, _P, _P]),
     "qim_mxfp8_gemm_ex": (_C, [_P, _P, _P, _P, _I, _I, _I, _C, _C, _P, _P, _P, _I, _P, _I, _P, _P]),
+    "qim_mxfp8_gemm_ws": (_C, [_P, _P, _P, _P, _I, _I, _I, _C, _C, _P, _P, _P, _I, _P, _I, _P, _P, _I, _P]),
+    "qim_mxfp8_gemm_ws_bytes": (_I, [_I, _I, _I, _C]),
     "qim_mxfp8_gemm_qk_norm_rope": (_C, [_P, _P, _P, _P, _I, _I, _I, _C, _P, _P, _P, _I, _F, _F, _P, _I, _P]),
     "qim_mxfp8_gemm_qk_norm_rope_vt": (_C, [_P, _P, _P, _P, _I, _I, _I, _C, _P, _P, _P, _I, _F, _F, _P, _I, _P,
                                            _P]),

@@ -87,6 +87,9 @@ def interleave_swiglu(gate_weight, up_weight, group=_native.SWIGLU_GROUP):
 _OUT_FORMATS = {torch.bfloat16: 0, torch.float32: _native.GEMM_OUT_F32, torch.float16: _native.GEMM_OUT_F16}
 
 
+_WS_EPILOGUES = (_native.EPI_NONE, _native.EPI_BIAS, _native.EPI_GATED_RESIDUAL)
+
+
 def mx_matmul(activation, weight_fp8, weight_scale, *, epilogue="none", bias=None, gate=None,
               residual=None, seq=None, out=None, weight_tiled=False, out_tiled=False, dtype=torch.bfloat16):
     """``activation @ weight.T`` in MXFP8 with a fused epilogue.
@@ -134,8 +137,16 @@ def mx_matmul(activation, weight_fp8, weight_scale, *, epilogue="none", bias=Non
         gate = gate.reshape(-1, n)
         if residual.shape != (m, n) or not residual.is_contiguous() or not gate.is_contiguous():
             raise ValueError("gated residual needs a contiguous (rows, N) residual and (B, N) gate")
-    _native.call("qim_mxfp8_gemm_ex", _native.ptr(a.values), _native.ptr(a.scales), _native.ptr(w),
-                 _native.ptr(weight_scale), m, n, k, epi, layouts, _native.ptr(bias), _native.ptr(gate),
-                 _native.ptr(residual), int(seq or m), _native.ptr(buf), ldo, _native.ptr(out_scales),
-                 _native.stream(dev))
+    args = (_native.ptr(a.values), _native.ptr(a.scales), _native.ptr(w), _native.ptr(weight_scale), m, n, k, epi,
+            layouts, _native.ptr(bias), _native.ptr(gate), _native.ptr(residual), int(seq or m), _native.ptr(buf),
+            ldo, _native.ptr(out_scales))
+    # A tile grid whose last partial round is a few quarter tiles splits them
+    # over K with a workspace from torch's caching allocator (stream-ordered,
+    # so reusing it for the next call on the stream is safe).
+    ws_bytes = _native.lib().qim_mxfp8_gemm_ws_bytes(m, n, k, epi) if epi in _WS_EPILOGUES else 0
+    if ws_bytes > 0:
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        _native.call("qim_mxfp8_gemm_ws", *args, _native.ptr(ws), ws_bytes, _native.stream(dev))
+    else:
+        _native.call("qim_mxfp8_gemm_ex", *args, _native.stream(dev))
     return result

@@ -740,6 +740,62 @@ def test_mxfp8_gemm_bias_config4(dev):
     assert rel_fro(yt.float().cpu().numpy()[rows], ref) < 1e-2
 
 
+def _gemm_unsplit(aq, wq, epi, layouts, out, ldo, bias=None, gate=None, res=None, seq=0):
+    """The same product through qim_mxfp8_gemm_ex: one workgroup per quarter
+    tile over all of K, no workspace."""
+    _native.call("qim_mxfp8_gemm_ex", _native.ptr(aq.values), _native.ptr(aq.scales), _native.ptr(wq.values),
+                 _native.ptr(wq.scales), aq.rows, wq.values.shape[0], wq.values.shape[1], epi, layouts,
+                 _native.ptr(bias), _native.ptr(gate), _native.ptr(res), seq or aq.rows, _native.ptr(out), ldo, None,
+                 _native.stream(out.device))
+
+
+@pytest.mark.parametrize("m,n,k", [(4352, 4096, 12288), (4352, 4096, 256), (4200, 4096, 384), (16640, 3072, 3072)])
+def test_mxfp8_gemm_split_tail(dev, m, n, k):
+    """Tile grids whose last partial round is a few quarter tiles (272 and 780
+    tiles on 256 CUs): mx_matmul splits those quarter tiles over K through a
+    workspace (qim_mxfp8_gemm_ws, then the summing epilogue launch).  Against
+    the unsplit call the fp32 products differ only by the order of the
+    partial sums, and the gated residual and bias outputs by at most that in
+    bf16; the split rows are checked against the oracle too."""
+    g = torch.Generator().manual_seed(11)
+    a = bf16_randn(g, (m, k))
+    w = bf16_randn(g, (n, k), 0.02)
+    ws_bytes = _native.lib().qim_mxfp8_gemm_ws_bytes(m, n, k, _native.EPI_GATED_RESIDUAL)
+    say("gemm split tail", m, n, k, ws_bytes)
+    assert ws_bytes > 0
+    aq, wq = mxfp8.quantize(a.to(dev)), mxfp8.quantize(w.to(dev))
+    # fp32 output, plain epilogue
+    before = _native.calls.get("qim_mxfp8_gemm_ws", 0)
+    y32 = gemm.mx_matmul(aq, wq.values, wq.scales, dtype=torch.float32)
+    assert _native.calls.get("qim_mxfp8_gemm_ws", 0) == before + 1
+    u32 = torch.empty_like(y32)
+    _gemm_unsplit(aq, wq, _native.EPI_NONE, _native.GEMM_OUT_F32, u32, n)
+    torch.cuda.synchronize()
+    d = (y32 - u32).abs().max().item()
+    assert d <= 1e-5 * u32.abs().max().item(), d
+    # sampled rows, the last ones among them, against the oracle
+    rows = np.unique(np.concatenate([np.random.default_rng(m).choice(m, 48, replace=False), np.arange(m - 16, m)]))
+    ref = O.mx_gemm(u8(aq.values), u8(aq.scales), u8(wq.values), u8(wq.scales), rows=rows)
+    assert rel_fro(y32.cpu().numpy()[rows], ref) < 1e-2
+    # gated residual (two batches) and bias, bf16
+    res = bf16_randn(g, (m, n)).to(dev)
+    gate = bf16_randn(g, (2, n)).tanh().to(dev)
+    seq = (m + 1) // 2
+    yg = gemm.mx_matmul(aq, wq.values, wq.scales, epilogue="gated_residual", gate=gate, residual=res, seq=seq)
+    ug = torch.empty_like(yg)
+    _gemm_unsplit(aq, wq, _native.EPI_GATED_RESIDUAL, 0, ug, n, gate=gate, res=res, seq=seq)
+    bias = bf16_randn(g, (n,), 0.01).to(dev)
+    yb = gemm.mx_matmul(aq, wq.values, wq.scales, epilogue="bias", bias=bias)
+    ub = torch.empty_like(yb)
+    _gemm_unsplit(aq, wq, _native.EPI_BIAS, 0, ub, n, bias=bias)
+    torch.cuda.synchronize()
+    for got, want in ((yg, ug), (yb, ub)):
+        # bf16 roundings of fp32 values that differ in the last bits: at most one ulp apart
+        diff = (got.float() - want.float()).abs()
+        assert (diff <= want.float().abs() * 2.0 ** -7 + 1e-30).all(), diff.max().item()
+        assert (diff > 0).float().mean().item() < 1e-2
+
+
 def test_mxfp8_gemm_gated_residual(dev):
     g = torch.Generator().manual_seed(3)
     m, n, k = 300, 512, 768

@@ -64,8 +64,8 @@ def test_teacher_forced_profiles(dev, monkeypatch):
         for case, r in by_case.items():
             print(profile, case, {k: round(v, 6) for k, v in r.items() if k != "per_step"}, r["per_step"],
                   flush=True)
-    assert {"qim_adaln", "qim_qk_norm_rope_pack", "qim_swiglu", "qim_adaln_quantize",
-            "qim_mxfp8_gemm_ex"} <= used, used
+    assert {"qim_adaln", "qim_qk_norm_rope_pack", "qim_swiglu", "qim_adaln_quantize"} <= used, used
+    assert used & {"qim_mxfp8_gemm_ex", "qim_mxfp8_gemm_ws"}, used
     for case in cases:
         control, fused, mx = rep["control"][case], rep["fused"][case], rep["mxfp8"][case]
         assert len(fused["per_step"]) == len(mx["per_step"]) == _SHAPE["steps"]

@@ -115,6 +115,9 @@ def test_abi_version():
     ("qim_mx_quantize", (16, 1 << 23, 1, 1 << 23, 16, 16, None), _native.QIM_ERR_SHAPE),
     ("qim_qk_norm_rope_pack", (16, 16, None, None, None, 16, 16, 16, 16, 16, None, 1, 4, 0, 1 << 30, 128,
                                1 << 37, 1e-6, 1e-6, None), _native.QIM_ERR_SHAPE),
+    # GEMM with a workspace: a misaligned workspace
+    ("qim_mxfp8_gemm_ws", (16, 16, 16, 16, 4352, 4096, 12288, 0, 0, None, None, None, 0, 16, 4096, None, 8, 1 << 24,
+                           None), _native.QIM_ERR_LAYOUT),
     # attention without a workspace: v required; a problem above the scratch array (S = T = 16640, 24 heads)
     ("qim_attention_noalloc", (16, 3072, 16, 3072, None, 3072, 16, 3072, 1, 256, 256, 24, 128, 0.1, None),
      _native.QIM_ERR_ARG),
@@ -135,6 +138,32 @@ def test_call_raises_unsupported_and_qimerror():
         _native.call("qim_mx_quantize", 16, 128, 1, 100, 16, 16, None)
     with pytest.raises(_native.QimError):
         _native.call("qim_mx_quantize", None, 0, 1, 128, None, None, None)
+
+
+def test_gemm_workspace_bytes():
+    """The split-K tail's workspace: 64 KiB of fp32 partial sums per quarter
+    tile and K-split, for the plain, bias and gated-residual epilogues when the
+    last partial round is at most CUs / 2 quarter tiles (256 CUs, the value
+    assumed without a GPU); splits fill one round of the CUs, at most one
+    stage pair (K = 128) each and at most 8."""
+    lib = _native.lib()
+    part = 64 * 1024
+    gr, bias, none, swq = _native.EPI_GATED_RESIDUAL, _native.EPI_BIAS, _native.EPI_NONE, _native.EPI_SWIGLU_QUANT
+    # 17 x 16 = 272 tiles: a tail of 16 tiles = 64 quarters, 4 splits each
+    assert lib.qim_mxfp8_gemm_ws_bytes(4352, 4096, 12288, gr) == 64 * 4 * part
+    assert lib.qim_mxfp8_gemm_ws_bytes(4352, 4096, 4096, none) == 64 * 4 * part
+    # K = 256 is two stage pairs: two splits
+    assert lib.qim_mxfp8_gemm_ws_bytes(4352, 4096, 256, bias) == 64 * 2 * part
+    # 65 x 12 = 780 tiles (2048^2 out- and down-projections): 12 tail tiles, 48 quarters, 5 splits
+    assert lib.qim_mxfp8_gemm_ws_bytes(16640, 3072, 12288, gr) == 48 * 5 * part
+    # no tail (204 tiles), a tail of 192 quarters (one split), a split-less epilogue, a last 128-column block,
+    # and shapes the GEMM rejects
+    assert lib.qim_mxfp8_gemm_ws_bytes(4352, 3072, 12288, gr) == 0
+    assert lib.qim_mxfp8_gemm_ws_bytes(4352, 12288, 3072, bias) == 0
+    assert lib.qim_mxfp8_gemm_ws_bytes(4352, 8192, 4096, swq) == 0
+    assert lib.qim_mxfp8_gemm_ws_bytes(4352, 4224, 4096, none) == 0
+    assert lib.qim_mxfp8_gemm_ws_bytes(4352, 4096, 100, none) == 0
+    assert lib.qim_mxfp8_gemm_ws_bytes(0, 4096, 4096, none) == 0
 
 
 def test_attention_workspace_bytes():
