@@ -922,12 +922,15 @@ __device__ __forceinline__ void qstep(const GemmArgs &p, const QPlan &Q, uint8_t
 }
 
 // fp32 words of one split-K partial: a quarter tile's 4 waves x 2 x 2 MFMA
-// tiles x 16 accumulators x 64 lanes, in register order (each store and load
-// instruction covers 256 contiguous bytes).
+// tiles x 16 accumulators x 64 lanes.  Each MFMA tile's 16 accumulators are
+// four groups of 4 (r = 4 g .. 4 g + 3), a group stored as 64 lanes x 16 bytes,
+// so each 16-byte store and load instruction covers 1 KiB contiguous.
 constexpr int QPART_WORDS = 4 * 2 * 2 * 16 * 64;
 
-__device__ __forceinline__ float *qpart(const GemmArgs &p, int unit, int wave, int i, int j, int r, int lane) {
-    return p.ws + (int64_t)unit * QPART_WORDS + (((wave * 2 + i) * 2 + j) * 16 + r) * 64 + lane;
+// Group 0 of the lane's accumulators of MFMA tile (i, j) of a wave; group g
+// is at [64 * g].
+__device__ __forceinline__ float4 *qpart(const GemmArgs &p, int unit, int wave, int i, int j, int lane) {
+    return reinterpret_cast<float4 *>(p.ws + (int64_t)unit * QPART_WORDS) + ((wave * 2 + i) * 2 + j) * 256 + lane;
 }
 
 // Corner of quarter tile q (of the last whole tiles, or a 128-row piece of a
@@ -985,9 +988,13 @@ __device__ __forceinline__ void quarter_tile(const GemmArgs &p, uint8_t *lds, ui
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < 2; ++j) {
+                float4 *w = qpart(p, u, wave, i, j, lane);
 #pragma unroll
-                for (int r = 0; r < 16; ++r) *qpart(p, u, wave, i, j, r, lane) = acc[i][j][r];
+                for (int g = 0; g < 4; ++g)
+                    w[64 * g] = make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                                            acc[i][j][4 * g + 3]);
+            }
         return;
     }
     block_barrier();
@@ -1041,40 +1048,64 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     epilogue<EPI, 4, 4>(p, acc, lds, tab, m0 + wm * 128, n0 + wn * 128, lane, wave);
 }
 
-// The split-K tail's second launch: one workgroup per quarter tile sums its
-// ksplit partials in order kp = 0, 1, ... (the register layout the quarter
-// tile's waves wrote) and runs the quarter tile's epilogue on them.  (One
-// one-wave workgroup per 64 x 64 block instead, four times as many, took
-// 48.5 us against 7.8 us at 64 quarter tiles x 4 splits.)
-constexpr int TAIL_LDS_BYTES = 4 * 16 * (64 * 8 + 8 * 16);  // epilogue<EPI, 2, 2>'s staging (TJ = 2, bf16 rows)
+// The split-K tail's second launch: one one-wave workgroup per 64 x 64 block
+// of a quarter tile (workgroup 4 q + w does wave w's block of quarter q) sums
+// its ksplit partials in order kp = 0, 1, ... (the register layout the
+// quarter tile's wave wrote, each partial's 16 loads in flight together) and
+// runs that block's epilogue.  At 64 quarter tiles x 4 splits this takes
+// 6.8 us, against 7.8 us with one four-wave workgroup per quarter tile.
+constexpr int TAIL_LDS_BYTES = 16 * (64 * 8 + 8 * 16);  // epilogue<EPI, 2, 2>'s staging of one wave (TJ = 2, bf16 rows)
 
 template <int EPI>
-__global__ __launch_bounds__(256) void k_mx_gemm_tail(GemmArgs p) {
+__global__ __launch_bounds__(64) void k_mx_gemm_tail(GemmArgs p) {
     static_assert(ring_offset<EPI>() == 0, "the split tail runs the plain, bias and gated-residual epilogues");
     __shared__ __attribute__((aligned(16))) uint8_t lds[TAIL_LDS_BYTES];
-    const int q = (int)blockIdx.x;
+    const int q = (int)(blockIdx.x >> 2);
     int64_t m0, n0;
     quarter_origin(p, q, m0, n0);
     if (m0 >= p.Mp) return;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lane = threadIdx.x, wave = (int)(blockIdx.x & 3);
     const int wm = wave >> 1, wn = wave & 1;
     f32x16_t acc[2][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < 2; ++j) {
+            const float4 *w = qpart(p, q, wave, i, j, lane);
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = *qpart(p, q, wave, i, j, r, lane);
+            for (int g = 0; g < 4; ++g) {
+                const float4 v = w[64 * g];
+                acc[i][j][4 * g] = v.x;
+                acc[i][j][4 * g + 1] = v.y;
+                acc[i][j][4 * g + 2] = v.z;
+                acc[i][j][4 * g + 3] = v.w;
+            }
+        }
     for (int kp = 1; kp < p.ksplit; ++kp) {
+        // all 16 loads of a partial in flight before its adds
         const int u = kp * p.quarters + q;
+        float4 v[2][2][4];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const float4 *w = qpart(p, u, wave, i, j, lane);
+#pragma unroll
+                for (int g = 0; g < 4; ++g) v[i][j][g] = w[64 * g];
+            }
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int j = 0; j < 2; ++j)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) acc[i][j][r] += *qpart(p, u, wave, i, j, r, lane);
+                for (int g = 0; g < 4; ++g) {
+                    acc[i][j][4 * g] += v[i][j][g].x;
+                    acc[i][j][4 * g + 1] += v[i][j][g].y;
+                    acc[i][j][4 * g + 2] += v[i][j][g].z;
+                    acc[i][j][4 * g + 3] += v[i][j][g].w;
+                }
     }
-    epilogue<EPI, 2, 2>(p, acc, lds, nullptr, m0 + wm * 64, n0 + wn * 64, lane, wave);
+    epilogue<EPI, 2, 2>(p, acc, lds, nullptr, m0 + wm * 64, n0 + wn * 64, lane, 0);  // LDS region 0: its own
 }
 
 // CUs the work split plans for: the current device's, or MI355X's 256 when no
@@ -1105,7 +1136,7 @@ static int launch_gemm(const GemmArgs &a, hipStream_t st) {
     const int64_t grid = a.main_tiles + a.quarters * split + half_column;
     launch(k_mx_gemm<EPI>, dim3((unsigned)grid), dim3(256), lds_bytes, st, a);
     if constexpr (ring_offset<EPI>() == 0 && EPI != QIM_EPI_QK_NORM_ROPE && EPI != EPI_QKV_VT) {
-        if (split > 1) launch(k_mx_gemm_tail<EPI>, dim3((unsigned)a.quarters), dim3(256), 0, st, a);
+        if (split > 1) launch(k_mx_gemm_tail<EPI>, dim3((unsigned)a.quarters * 4), dim3(64), 0, st, a);
     }
     return QIM_OK;
 }
